@@ -1,0 +1,113 @@
+/*
+ * libsage_capi: C ABI of the MI355X (gfx950) SageAttention path.
+ *
+ * This library replaces the reference's native launch boundary: rdna4_sage loads ahead-of-time code objects and
+ * launches them with hipModuleLaunchKernel and a packed kernarg block per manifest entry
+ * (src/rdna4_sage/_hip.py:52-73, kernel_build/build_kernels.py:330-333).  Here each of those launches is a typed C
+ * entry point that takes plain device pointers, sizes and element strides, validates them on the host and launches
+ * hipcc-built gfx950 kernels on the caller's stream.  Arguments are passed by value (no shared packing buffer), so
+ * entry points are reentrant; nothing synchronises.
+ *
+ * Conventions
+ *  - Return value: SAGE_OK (0) or a SAGE_ERR_* code; sage_last_error() gives the message (thread-local).
+ *  - Memory: the caller owns every buffer (inputs, outputs, intermediates).  The library allocates nothing.
+ *  - Streams: `stream` is a hipStream_t (NULL = the default stream).
+ *  - Element strides: (batch, seq, head) strides in elements; the head_dim axis must be contiguous; input base
+ *    pointers 16-byte aligned and strides multiples of 8 elements (the quantizers load 16-byte vectors).
+ *  - dtype: SAGE_DTYPE_BF16 or SAGE_DTYPE_F16; head_dim 64 or 128.
+ *
+ * Intermediate layouts (device memory, all contiguous):
+ *  - Q8  int8  [B, H, Sq, D]              (head-major; the reference writes [B, Sq, H, D])
+ *  - QS  fp32  [B, H, Sq]                 per-token scale / D, times the sm_scale fold factor
+ *  - K8  int8  [B, Hkv, Skp, D]           Skp = sage_kv_pad(Skv); rows >= Skv are zero
+ *  - KS  fp32  [B, Hkv, Skp / 32]         one scale per 32 keys (not divided by D)
+ *  - V8T e4m3  [B, Hkv, D, Skp]           V * 448 / amax, transposed; inside every 64-key group key 8g + 4h + r is
+ *                                         stored at position 32h + 4g + r (the order the attention kernel's fp8 MFMA
+ *                                         operand wants); keys >= Skv are zero
+ *  - VS  fp32  [B, Hkv, D]                per-channel max |v| over the sequence
+ */
+#ifndef SAGE_CAPI_H
+#define SAGE_CAPI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAGE_OK 0
+#define SAGE_ERR_INVALID 1     /* bad pointer, size, stride or alignment */
+#define SAGE_ERR_UNSUPPORTED 2 /* head_dim / dtype / causal shape the kernels are not built for */
+#define SAGE_ERR_HIP 3         /* a HIP runtime call failed */
+
+#define SAGE_DTYPE_BF16 0
+#define SAGE_DTYPE_F16 1
+
+#define SAGE_KV_BLOCK 32  /* keys per K scale (kernel_build/build_kernels.py:326) */
+#define SAGE_KV_PAD 128   /* K8 / V8T rows are padded to a multiple of this */
+
+/* ABI version of this header (bumped on any signature change). */
+int sage_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* sage_last_error(void);
+
+/* Padded KV length Skp used by K8 / KS / V8T. */
+int sage_kv_pad(int skv);
+
+/* JSON description of the built kernels (architecture, head dims, tiles); static storage. */
+const char* sage_manifest_json(void);
+
+/*
+ * Hadamard-rotate Q over head_dim and quantize to int8 with one scale per token.
+ * Replaces the quant_q launch of src/rdna4_sage/_attention.py:125-126 (kernel kernel_build/sage_quant.py:246-261,
+ * kernarg "<4Q5i4x2Q", build_kernels.py:332) and folds the sm_scale multiply of _attention.py:130-131:
+ * QS = fp32(fp32(s / D) * qs_mul); pass qs_mul = 1.0f for the default scale.
+ * q: [B, Sq, H, D] addressed as q + b*sb + s*ss + h*sh.
+ */
+int sage_quant_q(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H, int Sq, int D, int dtype,
+                 float qs_mul, int8_t* q8, float* qs, void* stream);
+
+/*
+ * Per-channel max |v| over the sequence, fp32 [B, Hkv, D].  Replaces
+ * torch.linalg.vector_norm(v, ord=inf, dim=seq, dtype=float32) of src/rdna4_sage/_attention.py:120-121.
+ * vs is overwritten (the library clears it with a fill kernel first).
+ */
+int sage_v_amax(const void* v, int64_t sb, int64_t ss, int64_t sh, int B, int Hkv, int Skv, int D, int dtype,
+                float* vs, void* stream);
+
+/*
+ * Hadamard-rotate K and quantize to int8 (one scale per 32 keys); quantize V to E4M3 with the per-channel scale
+ * 448 / max(vs, 1e-30) and store it transposed.  Replaces the quant_kv launch of src/rdna4_sage/_attention.py:127-129
+ * (kernel kernel_build/sage_quant.py:264-283, kernarg "<7Q9i4x2Q", build_kernels.py:333).
+ */
+int sage_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss,
+                  int64_t vsh, int B, int Hkv, int Skv, int D, int dtype, const float* vs, int8_t* k8, float* ks,
+                  uint8_t* v8t, void* stream);
+
+/*
+ * int8 QK^T / fp8 PV flash attention with the reference's online softmax (lazy rescale, threshold 8 in log2
+ * units), causal (bottom-right aligned, requires Sq == Skv) and grouped-query heads (H % Hkv == 0).
+ * Replaces the attn launch of src/rdna4_sage/_attention.py:133-139 (kernarg "<4Q3i4x6Q2i", build_kernels.py:331).
+ * out: out + b*osb + s*oss + h*osh (element strides, head_dim contiguous), dtype out_dtype.
+ * lse: optional fp32 [B, H, Sq] (natural-log logsumexp of the quantized logits); pass NULL to skip.
+ */
+int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
+                  const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq,
+                  int Skv, int D, int causal, int out_dtype, float* lse, void* stream);
+
+/*
+ * The whole path in one call: v_amax, quant_q, quant_kv, attention, on one stream.  Replaces the body of
+ * src/rdna4_sage/_attention.py:97-140 below check_supported.  Intermediates are caller-owned buffers with the
+ * layouts above.
+ */
+int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
+                 int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb, int64_t oss,
+                 int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float qs_mul,
+                 int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAGE_CAPI_H */

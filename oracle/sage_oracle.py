@@ -1,0 +1,356 @@
+"""CPU restatement of the reference's quantized SageAttention math (numpy, float32 / float64).
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker for the gfx950 HIP path: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it.  The product path
+(``cdna4_sage``) never calls it and fails loudly when the HIP library is missing.
+
+What each function restates (paths relative to the reference checkout):
+
+* ``hadamard_pm1``      src/rdna4_sage/_attention.py:48-56 (Sylvester +-1 matrix, order RB = head_dim for
+                        head_dim 64 / 128, kernel_build/build_kernels.py:336-337, :398-400).
+* ``fwht_rows``         the rotation x = row @ Hm of kernel_build/sage_quant.py:225-243 (`_load_qk`).  The
+                        reference accumulates the +-1 products in fp32 inside ``tl.dot`` in an order that the
+                        gfx12 hardware fixes and that is not recoverable here.  This build defines the rotation
+                        as a float64 fast Walsh-Hadamard transform in a fixed stage order (stage bit 0 first,
+                        then 1, 2, ...; butterfly (a, b) -> (a + b, a - b)), rounded once to float32.  For bf16
+                        and fp16 rows every float64 partial sum is exact unless a row spans more than ~2^38 in
+                        magnitude, so the result is the correctly rounded fp32 of the exact sum; it equals the
+                        reference's fp32 accumulation whenever that accumulation is exact.  The HIP kernels run
+                        the same stages in the same order, so the two agree bit for bit in every case.
+* ``quant_q``           kernel_build/sage_quant.py:246-261 (`_quant_q`) plus the sm_scale fold of
+                        src/rdna4_sage/_attention.py:130-131.
+* ``v_amax``            src/rdna4_sage/_attention.py:120-121 (`vector_norm(v, inf, dim=seq, dtype=fp32)`).
+* ``quant_kv``          kernel_build/sage_quant.py:264-283 (`_quant_kv`).
+* ``f32_to_e4m3``       the fp32 -> float8 E4M3FN cast of sage_quant.py:283 (round to nearest even, subnormals
+                        kept; inputs are clamped to +-448 first so the NaN code is never produced).
+* ``attention``         the FlyDSL kernel's math as rewritten by kernel_build/make_sage.py:75-107, :196-237,
+                        make_sage_r2.py:54-269 and make_sage_pkg.py:74-87: int32 S = Q8 K8^T, per-32-key K scale,
+                        lazy rescale with threshold 8.0 (log2 units), exp2, P cast to E4M3, fp32 PV
+                        accumulation, epilogue (O * ((1/448) / l)) * VS.  ``block_n`` is the KV tile of the
+                        online softmax: 32 in the reference (kernel_build/compile_attn.py:109), 64 in this
+                        build's gfx950 kernel.
+* ``lse_reference``     src/sageattention/core.py:36-57 (`_lse`).
+
+All float32 steps are written as float32 numpy operations, which round to nearest even like the GPU's
+float32 ALU.  ``exp2`` and the order of the fp32 additions inside the PV product are implementation-defined
+on both sides; the attention output is therefore compared with a tolerance, while Q8 / K8 / V8 and their
+scales are compared bit for bit.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F32 = np.float32
+KV_BLOCK = 32          # one K scale per 32 keys (kernel_build/build_kernels.py:326)
+E4M3_MAX = 448.0
+RESCALE_THRESHOLD = 8.0  # make_sage.py:219-225: keep a stale max until it is exceeded by 2^8
+LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# bf16 / fp16 helpers (inputs are kept as float32 arrays holding exactly representable bf16 / fp16 values)
+# ----------------------------------------------------------------------------------------------------------
+def round_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bf16 value (RNE), returned as float32."""
+    b = np.ascontiguousarray(x, dtype=F32).view(np.uint32).astype(np.uint64)
+    rounded = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    nan = np.isnan(x)
+    out = rounded.astype(np.uint32).view(F32).copy()
+    out[nan] = np.nan
+    return out
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(F32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    return (round_to_bf16(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Hadamard rotation
+# ----------------------------------------------------------------------------------------------------------
+def hadamard_pm1(d: int) -> np.ndarray:
+    """Sylvester +-1 matrix of order d (src/rdna4_sage/_attention.py:48-56): H1 = [1], H2n = [[H, H], [H, -H]]."""
+    h = np.ones((1, 1), dtype=np.float64)
+    while h.shape[0] < d:
+        h = np.block([[h, h], [h, -h]])
+    return h
+
+
+def fwht_rows(x: np.ndarray) -> np.ndarray:
+    """Rotate the last axis by the unnormalised Sylvester Hadamard matrix (x @ H, H symmetric).
+
+    float64 butterflies, stage bit 0 first; returns float64 (round with ``.astype(np.float32)``)."""
+    x = np.array(x, dtype=np.float64, copy=True)
+    d = x.shape[-1]
+    assert d & (d - 1) == 0, "power-of-two head_dim only"
+    lead = x.shape[:-1]
+    s = 1
+    while s < d:
+        v = x.reshape(*lead, d // (2 * s), 2, s)
+        a = v[..., 0, :].copy()
+        b = v[..., 1, :]
+        v[..., 0, :] = a + b
+        v[..., 1, :] = a - b
+        s *= 2
+    return x
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Rounding helpers
+# ----------------------------------------------------------------------------------------------------------
+def round_half_away_i8(y: np.ndarray) -> np.ndarray:
+    """int8(trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)))  (sage_quant.py:257, :278)."""
+    y = y.astype(F32)
+    t = np.where(y >= 0, y + F32(0.5), y - F32(0.5)).astype(F32)
+    return np.trunc(t).astype(np.int8)
+
+
+def f32_to_e4m3(y: np.ndarray) -> np.ndarray:
+    """float32 -> OCP float8 E4M3FN bits (uint8), round to nearest even, subnormals kept.
+
+    Inputs must already lie in [-448, 448] (the quantizer clamps); NaN is never produced."""
+    y = np.ascontiguousarray(y, dtype=F32)
+    bits = y.view(np.uint32)
+    sign = ((bits >> 31) & 1).astype(np.uint32) << 7
+    a = np.abs(y)
+    out = np.zeros(y.shape, dtype=np.uint32)
+    normal = a >= F32(2.0 ** -6)
+    # normal range: round the 23-bit mantissa to 3 bits (RNE) and rebias the exponent (127 -> 7)
+    ab = a.view(np.uint32).astype(np.uint64)
+    r = (ab + 0x7FFFF + ((ab >> 20) & 1)) >> 20
+    nrm = (r - ((127 - 7) << 3)).astype(np.uint32)
+    # subnormal range: value = m * 2^-9, m = RNE(a * 512) in 0..8 (8 is the smallest normal, code 0x08)
+    sub = np.rint(a * F32(512.0)).astype(np.uint32)
+    out = np.where(normal, nrm, sub)
+    return (out | sign).astype(np.uint8)
+
+
+def e4m3_to_f32(bits: np.ndarray) -> np.ndarray:
+    """OCP E4M3FN bits -> float32 (0x7F / 0xFF decode to NaN)."""
+    b = np.asarray(bits, dtype=np.uint8).astype(np.int32)
+    s = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    val = np.where((b & 0x7F) == 0x7F, np.nan, val)
+    return (s * val).astype(F32)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Quantizers
+# ----------------------------------------------------------------------------------------------------------
+def qs_fold_factor(sm_scale, d: int):
+    """None for the default scale, else fp32(sm_scale * sqrt(D)) (src/rdna4_sage/_attention.py:130-131)."""
+    if sm_scale is None or sm_scale <= 0 or math.isclose(sm_scale, d ** -0.5, rel_tol=1e-6):
+        return None
+    return F32(sm_scale * math.sqrt(d))
+
+
+def quant_q(q: np.ndarray, sm_scale=None):
+    """q: [B, H, S, D] float32 holding bf16/fp16 values (HND).
+
+    Returns (q8 int8 [B, H, S, D], qs float32 [B, H, S]).  sage_quant.py:246-261; scale / RB because the
+    unnormalised Hadamard multiplies Q K^T by RB (:259-260); optional sm_scale fold (_attention.py:130-131)."""
+    d = q.shape[-1]
+    x = fwht_rows(q).astype(F32)
+    a = np.maximum(np.abs(x).max(axis=-1), F32(1e-12)).astype(F32)
+    s = (a / F32(127.0)).astype(F32)
+    y = (x / s[..., None]).astype(F32)
+    q8 = round_half_away_i8(y)
+    qs = (s / F32(d)).astype(F32)
+    f = qs_fold_factor(sm_scale, d)
+    if f is not None:
+        qs = (qs * f).astype(F32)
+    return q8, qs
+
+
+def v_amax(v: np.ndarray) -> np.ndarray:
+    """v: [B, Hkv, S, D] -> per-channel max |v| over the sequence, float32 [B, Hkv, D] (_attention.py:120-121)."""
+    if v.shape[2] == 0:
+        return np.zeros(v.shape[:2] + v.shape[3:], dtype=F32)
+    return np.abs(v.astype(F32)).max(axis=2).astype(F32)
+
+
+def padded_len(s: int, multiple: int = 64) -> int:
+    return (s + multiple - 1) // multiple * multiple
+
+
+def quant_kv(k: np.ndarray, v: np.ndarray, vs: np.ndarray | None = None, seq_pad: int | None = None):
+    """k, v: [B, Hkv, S, D] float32 holding bf16/fp16 values.
+
+    Returns (k8 int8 [B, Hkv, Sp, D], ks float32 [B, Hkv, Sp/32], v8 uint8 E4M3 bits [B, Hkv, Sp, D],
+    vs float32 [B, Hkv, D]) in natural key order; rows >= S are zero.  sage_quant.py:264-283."""
+    B, Hkv, S, D = k.shape
+    sp = padded_len(S, KV_BLOCK) if seq_pad is None else seq_pad
+    assert sp % KV_BLOCK == 0 and sp >= S
+    if vs is None:
+        vs = v_amax(v)
+    kp = np.zeros((B, Hkv, sp, D), dtype=F32)
+    kp[:, :, :S] = k
+    x = fwht_rows(kp).astype(F32).reshape(B, Hkv, sp // KV_BLOCK, KV_BLOCK, D)
+    a = np.maximum(np.abs(x).max(axis=(-1, -2)), F32(1e-12)).astype(F32)
+    ks = (a / F32(127.0)).astype(F32)
+    y = (x / ks[..., None, None]).astype(F32)
+    k8 = round_half_away_i8(y).reshape(B, Hkv, sp, D)
+    vsc = np.maximum(vs.astype(F32), F32(1e-30))
+    c = (F32(448.0) / vsc).astype(F32)
+    vp = np.zeros((B, Hkv, sp, D), dtype=F32)
+    vp[:, :, :S] = v
+    yv = np.clip((vp * c[:, :, None, :]).astype(F32), F32(-448.0), F32(448.0))
+    v8 = f32_to_e4m3(yv)
+    return k8, ks, v8, vs.astype(F32)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Attention (tile-faithful float32 emulation)
+# ----------------------------------------------------------------------------------------------------------
+def logit_scale_base(d: int) -> np.float32:
+    """fp32(sm_scale * LOG2E) with the kernel's built-in sm_scale = 1/sqrt(D) (make_sage.py:40-46, :76-80)."""
+    return F32((1.0 / math.sqrt(d)) * LOG2E)
+
+
+def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n: int = 32,
+              out_dtype: str = "bf16", threshold: float = RESCALE_THRESHOLD, return_stats: bool = False):
+    """Quantized attention as the reference kernel computes it.
+
+    q8 [B, H, Sq, D] int8, qs [B, H, Sq] f32, k8 [B, Hkv, Sp, D] int8, ks [B, Hkv, Sp/32] f32,
+    v8 [B, Hkv, Sp, D] E4M3 bits (natural key order), vs [B, Hkv, D] f32.  Returns float32 [B, H, Sq, D]
+    holding values rounded to ``out_dtype`` ("bf16", "f16" or "f32" for no rounding)."""
+    B, H, Sq, D = q8.shape
+    Hkv, Sp = k8.shape[1], k8.shape[2]
+    assert block_n % KV_BLOCK == 0 and H % Hkv == 0
+    grp = H // Hkv
+    c0 = logit_scale_base(D)
+    cl = (c0 * qs.astype(F32)).astype(F32)                      # [B, H, Sq]
+    q8f = q8.astype(F32)
+    k8f = k8.astype(F32)
+    v8f = e4m3_to_f32(v8)
+    m = np.full((B, H, Sq), -np.inf, dtype=F32)
+    l = np.zeros((B, H, Sq), dtype=F32)
+    o = np.zeros((B, H, Sq, D), dtype=F32)
+    rows = np.arange(Sq)
+    causal_off = seq_kv - Sq
+    nsub = block_n // KV_BLOCK
+    n_tiles = (seq_kv + block_n - 1) // block_n
+    hk = np.arange(H) // grp
+    for t in range(n_tiles):
+        j0 = t * block_n
+        j1 = min(j0 + block_n, Sp)
+        cols = np.arange(j0, j0 + block_n)
+        kt = np.zeros((B, Hkv, block_n, D), dtype=F32)
+        kt[:, :, : j1 - j0] = k8f[:, :, j0:j1]
+        vt = np.zeros((B, Hkv, block_n, D), dtype=F32)
+        vt[:, :, : j1 - j0] = v8f[:, :, j0:j1]
+        # exact int32 scores (|S| <= 127*127*128 < 2^24, so float32 matmul is exact)
+        s = np.matmul(q8f, np.swapaxes(kt[:, hk], -1, -2))      # [B, H, Sq, block_n]
+        mask = cols[None, :] >= seq_kv
+        if causal:
+            mask = mask | (cols[None, :] > rows[:, None] + causal_off)
+        s = np.where(mask, F32(-np.inf), s).astype(F32)
+        kst = np.ones((B, Hkv, nsub), dtype=F32)
+        nb = min(nsub, ks.shape[2] - j0 // KV_BLOCK)
+        kst[:, :, :nb] = ks[:, :, j0 // KV_BLOCK: j0 // KV_BLOCK + nb]
+        kst = kst[:, hk]                                          # [B, H, nsub]
+        sb = s.reshape(B, H, Sq, nsub, KV_BLOCK)
+        rowmax = (sb.max(axis=-1) * kst[:, :, None, :]).astype(F32).max(axis=-1)   # [B, H, Sq]
+        m_cand = np.maximum(m, rowmax)
+        with np.errstate(invalid="ignore"):
+            need = ((m_cand - m).astype(F32) * cl).astype(F32) > F32(threshold)
+        m_new = np.where(need, m_cand, m).astype(F32)
+        with np.errstate(invalid="ignore"):
+            corr = np.exp2(((m - m_new).astype(F32) * cl).astype(F32)).astype(F32)
+        neg = (F32(0.0) - (cl * m_new).astype(F32)).astype(F32)
+        ct = (cl[..., None] * kst[:, :, None, :]).astype(F32)    # [B, H, Sq, nsub]
+        arg = (sb.astype(np.float64) * ct[..., None].astype(np.float64) + neg[..., None, None]).astype(F32)
+        p = np.exp2(arg).astype(F32).reshape(B, H, Sq, block_n)
+        tile_sum = p.sum(axis=-1, dtype=F32)
+        l = ((corr * l).astype(F32) + tile_sum).astype(F32)
+        o = np.where(need[..., None], (o * corr[..., None]).astype(F32), o)
+        p8 = e4m3_to_f32(f32_to_e4m3(p))
+        o = (o + np.matmul(p8, vt[:, hk])).astype(F32)
+        m = m_new
+    inv = (F32(1.0 / 448.0) / l).astype(F32)
+    out = ((o * inv[..., None]).astype(F32) * vs[:, hk][:, :, None, :].astype(F32)).astype(F32)
+    out = round_output(out, out_dtype)
+    if return_stats:
+        return out, m, l
+    return out
+
+
+def round_output(x: np.ndarray, out_dtype: str) -> np.ndarray:
+    if out_dtype == "bf16":
+        return round_to_bf16(x)
+    if out_dtype == "f16":
+        return x.astype(np.float16).astype(F32)
+    return x.astype(F32)
+
+
+def sage_forward(q, k, v, causal=False, sm_scale=None, block_n=32, out_dtype="bf16"):
+    """Full quantized path on HND float32 arrays holding bf16 / fp16 values: quant_q, quant_kv, attention."""
+    q8, qs = quant_q(q, sm_scale)
+    k8, ks, v8, vs = quant_kv(k, v)
+    return attention(q8, qs, k8, ks, v8, vs, k.shape[2], causal=causal, block_n=block_n, out_dtype=out_dtype)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Textbook references used to bound the emulation
+# ----------------------------------------------------------------------------------------------------------
+def sdpa_reference(q, k, v, causal=False, sm_scale=None):
+    """float64 softmax attention, bottom-right causal, GQA by head repetition."""
+    B, H, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    rep = H // Hkv
+    kk = np.repeat(k.astype(np.float64), rep, axis=1)
+    vv = np.repeat(v.astype(np.float64), rep, axis=1)
+    scale = D ** -0.5 if sm_scale is None else sm_scale
+    s = np.matmul(q.astype(np.float64), np.swapaxes(kk, -1, -2)) * scale
+    if causal:
+        mask = np.arange(Skv)[None, :] > np.arange(Sq)[:, None] + (Skv - Sq)
+        s = np.where(mask, -np.inf, s)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, vv)
+
+
+def lse_reference(q, k, causal=False, sm_scale=None):
+    """logsumexp_j(q_i . k_j * scale) in float64 (src/sageattention/core.py:36-57), [B, H, Sq]."""
+    B, H, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    kk = np.repeat(k.astype(np.float64), H // Hkv, axis=1)
+    scale = D ** -0.5 if sm_scale is None else sm_scale
+    s = np.matmul(q.astype(np.float64), np.swapaxes(kk, -1, -2)) * scale
+    if causal:
+        mask = np.arange(Skv)[None, :] > np.arange(Sq)[:, None] + (Skv - Sq)
+        s = np.where(mask, -np.inf, s)
+    mx = s.max(axis=-1, keepdims=True)
+    return (np.log(np.exp(s - mx).sum(axis=-1)) + mx[..., 0])
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Layout helpers shared with the tests (device layouts of the HIP path)
+# ----------------------------------------------------------------------------------------------------------
+def v8_to_device_layout(v8: np.ndarray) -> np.ndarray:
+    """Natural [B, Hkv, Sp, D] E4M3 -> the HIP path's transposed V8T [B, Hkv, D, Sp].
+
+    Within every 64-key group the keys are stored as the 4-key chunks of lane-half 0 first
+    (keys 8g + 0..3, g = 0..7), then those of lane-half 1 (keys 8g + 4..7): key 8g + 4h + r sits at
+    position 32h + 4g + r."""
+    B, Hkv, Sp, D = v8.shape
+    assert Sp % 64 == 0
+    t = np.swapaxes(v8, -1, -2)                                  # [B, Hkv, D, Sp]
+    t = t.reshape(B, Hkv, D, Sp // 64, 8, 2, 4)                  # key = 64G + 8g + 4h + r
+    t = np.swapaxes(t, -3, -2)                                   # -> [.., G, h, g, r]
+    return np.ascontiguousarray(t.reshape(B, Hkv, D, Sp))
+
+
+def v8_from_device_layout(v8t: np.ndarray) -> np.ndarray:
+    B, Hkv, D, Sp = v8t.shape
+    t = v8t.reshape(B, Hkv, D, Sp // 64, 2, 8, 4)
+    t = np.swapaxes(t, -3, -2).reshape(B, Hkv, D, Sp)
+    return np.ascontiguousarray(np.swapaxes(t, -1, -2))

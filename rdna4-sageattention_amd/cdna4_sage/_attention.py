@@ -1,0 +1,124 @@
+"""int8 QK / fp8 PV attention for MI355X (gfx950): quantize Q, K, V and run the CDNA4 kernel.
+
+Mirrors src/rdna4_sage/_attention.py (same names, arguments and error behaviour) with the launch boundary moved into
+libsage_capi.so: one C call runs V amax, the Q quantizer, the K/V quantizer and the attention kernel on torch's
+current stream.  Intermediates are torch-owned (caching allocator), as in the reference (_attention.py:115-133).
+"""
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import torch
+
+from . import _capi
+
+_MANIFEST_PATH = Path(__file__).resolve().parent / "manifest.json"
+_MANIFEST = json.loads(_MANIFEST_PATH.read_text())
+KV_BLOCK = _MANIFEST["kv_block"]            # keys per K scale (reference: kernels/manifest.json "kv_block")
+HEAD_DIMS = tuple(_MANIFEST["head_dims"])
+ARCHS = (_MANIFEST["arch"],)
+DTYPES = {torch.bfloat16: _capi.DTYPE_BF16, torch.float16: _capi.DTYPE_F16}
+_I32_MAX = 2**31 - 1
+
+_arch_cache = {}
+
+
+class Unsupported(Exception):
+    """The inputs fall outside what the gfx950 kernels handle; use another attention backend."""
+
+
+def device_arch(device: torch.device) -> str:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _arch_cache:
+        _arch_cache[idx] = torch.cuda.get_device_properties(idx).gcnArchName.split(":")[0]
+    return _arch_cache[idx]
+
+
+def _bsh(t: torch.Tensor, layout: str):
+    """(batch, seq, head) element strides.  The quantizers load 16-byte vectors, so the base must be 16-byte aligned
+    and the strides multiples of 8 elements; anything else is made contiguous (reference: _attention.py:59-67)."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16:
+        t = t.contiguous()
+    st = (t.stride(0), t.stride(2), t.stride(1)) if layout == "HND" else (t.stride(0), t.stride(1), t.stride(2))
+    if any(s % 8 for s in st):
+        t = t.contiguous()
+        st = (t.stride(0), t.stride(2), t.stride(1)) if layout == "HND" else (t.stride(0), t.stride(1), t.stride(2))
+    return t, st
+
+
+def check_supported(q, k, v, layout, is_causal=False):
+    """Raise Unsupported with the reason if the gfx950 kernels cannot run these inputs (reference:
+    _attention.py:70-94, with the architecture set {gfx950} and head dims {64, 128})."""
+    if layout not in ("HND", "NHD"):
+        raise Unsupported(f"layout {layout!r}")
+    if not (q.is_cuda and k.device == q.device and v.device == q.device):
+        raise Unsupported("tensors must be on one ROCm GPU")
+    if q.dtype not in DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise Unsupported(f"dtype {q.dtype}/{k.dtype}/{v.dtype} (fp16 or bf16 required)")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise Unsupported("4D tensors required")
+    arch = device_arch(q.device)
+    if arch not in ARCHS:
+        raise Unsupported(f"GPU {arch} is not CDNA4 (kernels built for {', '.join(ARCHS)} only)")
+    hd = q.shape[-1]
+    if hd not in HEAD_DIMS or k.shape[-1] != hd or v.shape[-1] != hd:
+        raise Unsupported(f"head_dim {hd} (supported {HEAD_DIMS})")
+    h_ax, s_ax = (1, 2) if layout == "HND" else (2, 1)
+    if q.shape[0] != k.shape[0] or k.shape[0] != v.shape[0] or k.shape[h_ax] != v.shape[h_ax] or k.shape[s_ax] != v.shape[s_ax]:
+        raise Unsupported("q/k/v batch, k/v heads and k/v lengths must match")
+    if q.shape[h_ax] % k.shape[h_ax]:
+        raise Unsupported(f"heads {q.shape[h_ax]} not a multiple of kv heads {k.shape[h_ax]}")
+    if max(q.numel(), k.numel()) > _I32_MAX or k.shape[s_ax] == 0 or q.shape[s_ax] == 0:
+        raise Unsupported("tensor too large for 32-bit indexing or empty")
+    if is_causal and q.shape[s_ax] != k.shape[s_ax]:
+        raise Unsupported("causal attention needs q_len == kv_len")
+
+
+def qs_fold_factor(sm_scale, head_dim: int) -> float:
+    """Multiplier folded into the Q scales: the kernel has 1/sqrt(D) built in (reference: _attention.py:130-131)."""
+    if sm_scale is not None and not math.isclose(sm_scale, head_dim ** -0.5, rel_tol=1e-6):
+        return float(sm_scale * math.sqrt(head_dim))
+    return 1.0
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
+    """Attention without mask, optionally causal (q_len == kv_len).  q: (B, H, Sq, D) for "HND" or (B, Sq, H, D) for
+    "NHD"; k/v alike, with H a multiple of the kv head count.  Returns (B, Sq, H, D) contiguous in q's dtype."""
+    check_supported(q, k, v, layout, is_causal)
+    dev = q.device
+    if layout == "HND":
+        B, H, Sq, D = q.shape
+        Hkv, Skv = k.shape[1], k.shape[2]
+    else:
+        B, Sq, H, D = q.shape
+        Skv, Hkv = k.shape[1], k.shape[2]
+    dt = DTYPES[q.dtype]
+    q, sq_ = _bsh(q, layout)
+    k, sk_ = _bsh(k, layout)
+    v, sv_ = _bsh(v, layout)
+    skp = _capi.kv_pad(Skv)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    q8 = torch.empty((B, H, Sq, D), device=dev, dtype=torch.int8)
+    qs = torch.empty((B, H, Sq), device=dev, dtype=torch.float32)
+    k8 = torch.empty((B, Hkv, skp, D), device=dev, dtype=torch.int8)
+    ks = torch.empty((B, Hkv, skp // KV_BLOCK), device=dev, dtype=torch.float32)
+    v8t = torch.empty((B, Hkv, D, skp), device=dev, dtype=torch.uint8)
+    vs = torch.empty((B, Hkv, D), device=dev, dtype=torch.float32)
+    out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
+    with torch.cuda.device(dev):
+        _capi.call("sage_forward", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),
+                   B, H, Hkv, Sq, Skv, D, dt, int(bool(is_causal)), qs_fold_factor(sm_scale, D),
+                   _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(v8t), _ptr(vs), stream)
+    return out
+
+
+def _out_strides(out: torch.Tensor):
+    # out is (B, Sq, H, D): (batch, seq, head) element strides
+    return out.stride(0), out.stride(1), out.stride(2)

@@ -1,0 +1,80 @@
+"""ctypes binding of libsage_capi.so (the C ABI declared in include/sage_capi.h).
+
+Replaces the reference's driver-API FFI (src/rdna4_sage/_hip.py:141-213): instead of packing kernarg blocks into a
+shared ctypes buffer per kernel and calling hipModuleLaunchKernel, each launch is a typed C call with arguments
+passed by value, so concurrent callers cannot clobber each other's arguments.  torch is imported before the library
+is opened, so the library binds to the HIP runtime instance torch already loaded (same soname) and shares its device
+context and streams, which is the reason the reference looks the runtime up in /proc/self/maps (_hip.py:151-168).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime first)
+
+LIB_PATH = Path(__file__).resolve().parent / "libsage_capi.so"
+
+SAGE_OK, SAGE_ERR_INVALID, SAGE_ERR_UNSUPPORTED, SAGE_ERR_HIP = 0, 1, 2, 3
+DTYPE_BF16, DTYPE_F16 = 0, 1
+ABI_VERSION = 1
+
+_lib = None
+_lock = threading.Lock()
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+SIGNATURES = {
+    "sage_abi_version": ([], _I),
+    "sage_last_error": ([], ctypes.c_char_p),
+    "sage_kv_pad": ([_I], _I),
+    "sage_manifest_json": ([], ctypes.c_char_p),
+    "sage_quant_q": ([_P, _L, _L, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P], _I),
+    "sage_v_amax": ([_P, _L, _L, _L, _I, _I, _I, _I, _I, _P, _P], _I),
+    "sage_quant_kv": ([_P, _L, _L, _L, _P, _L, _L, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
+    "sage_attn_fwd": ([_P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "sage_forward": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
+                      _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P], _I),
+}
+
+
+class SageError(RuntimeError):
+    """A libsage_capi call returned an error code."""
+
+    def __init__(self, fn: str, code: int, message: str):
+        super().__init__(f"cdna4_sage: {fn} failed (code {code}): {message}")
+        self.code = code
+
+
+def lib():
+    """Open libsage_capi.so once (thread-safe).  Raises RuntimeError when the library has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(f"cdna4_sage: {LIB_PATH} is missing; build it with "
+                                       "`python -m cdna4_sage._build` (hipcc --offload-arch=gfx950)")
+                h = ctypes.CDLL(str(LIB_PATH))
+                for name, (args, res) in SIGNATURES.items():
+                    fn = getattr(h, name)
+                    fn.argtypes = args
+                    fn.restype = res
+                if h.sage_abi_version() != ABI_VERSION:
+                    raise RuntimeError(f"cdna4_sage: library ABI {h.sage_abi_version()} != expected {ABI_VERSION}")
+                _lib = h
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != SAGE_OK:
+        raise SageError(name, rc, lib().sage_last_error().decode(errors="replace"))
+
+
+def kv_pad(skv: int) -> int:
+    return int(lib().sage_kv_pad(int(skv)))

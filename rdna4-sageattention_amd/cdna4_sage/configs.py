@@ -1,0 +1,102 @@
+"""Seeded synthetic inputs for the benchmark configurations of this path.
+
+Every tensor is drawn on the CPU with ``torch.Generator().manual_seed(config index)`` (float32 normal samples, then
+rounded to the target dtype) so a CPU checker sees exactly the bits the GPU receives.  Distributions are written as
+N(mean, variance): N(0, 3) has standard deviation sqrt(3).
+
+  1  HND [1, 8, 1024, 64] bf16, Q, K, V ~ N(0, 1)                               (plumbing; below MIN_WORK)
+  2  HND [1, 24, 4608, 128] bf16, Q, V ~ N(0, 1); K ~ N(0, 1) + offset[c] on 8 random channels, offset ~ N(0, 3)
+     shared over tokens and heads                                                 (Flux joint attention)
+  3  HND [1, 40, 32760, 128] bf16, N(0, 1); ceil(0.02 * 128) = 3 random channels x10 in K and in V  (Wan 2.1 14B)
+  4  HND [1, 24, 67320, 128] bf16, Q, K, V ~ N(0, 0.5^2); K += bias[c] ~ N(0, 2) shared over tokens and heads
+                                                                                  (HunyuanVideo)
+  5a Q [2, 32, 8192, 128], K/V [2, 8, 8192, 128] bf16, N(0, 1), causal, return_lse  (GQA 4)
+  5b Q [2, 16, 8192, 64],  K/V [2, 4, 8192, 64]  bf16, N(0, 1), causal, return_lse
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class Config:
+    name: str
+    seed: int
+    B: int
+    H: int
+    Hkv: int
+    S: int
+    D: int
+    causal: bool = False
+    return_lse: bool = False
+    dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def shape_q(self):
+        return (self.B, self.H, self.S, self.D)
+
+    @property
+    def shape_kv(self):
+        return (self.B, self.Hkv, self.S, self.D)
+
+    def pairs(self) -> int:
+        """(query, key) pairs per head: S^2, or S(S+1)/2 for causal."""
+        return self.S * (self.S + 1) // 2 if self.causal else self.S * self.S
+
+    def attention_ops(self) -> int:
+        """Algorithmic int8 + fp8 MFMA ops: QK^T and PV, 2 ops per multiply-add each."""
+        return 4 * self.B * self.H * self.pairs() * self.D
+
+    def quant_q_bytes(self) -> int:
+        n = self.B * self.H * self.S
+        return n * self.D * (2 + 1) + 4 * n
+
+    def quant_kv_bytes(self, kv_pad: int) -> int:
+        n = self.B * self.Hkv
+        return (2 * n * self.S * self.D * 2 + 2 * n * kv_pad * self.D + 4 * n * kv_pad // 32 + 4 * n * self.D)
+
+
+CONFIGS = {
+    "1": Config("plumbing 1x8x1024x64", 1, 1, 8, 8, 1024, 64),
+    "2": Config("flux 1x24x4608x128", 2, 1, 24, 24, 4608, 128),
+    "3": Config("wan14b 1x40x32760x128", 3, 1, 40, 40, 32760, 128),
+    "4": Config("hunyuan 1x24x67320x128", 4, 1, 24, 24, 67320, 128),
+    "5a": Config("causal-gqa 2x32/8x8192x128", 5, 2, 32, 8, 8192, 128, causal=True, return_lse=True),
+    "5b": Config("causal-gqa 2x16/4x8192x64", 5, 2, 16, 4, 8192, 64, causal=True, return_lse=True),
+}
+
+
+def _normal(g, shape, std=1.0):
+    return torch.randn(shape, generator=g, dtype=torch.float32) * std
+
+
+def make_inputs(cfg: Config, heads: slice | None = None):
+    """CPU tensors (q, k, v) in HND layout and cfg.dtype.  ``heads`` restricts the returned KV heads (and the query
+    heads that read them) after drawing the full tensors, so a sample matches the full problem bit for bit."""
+    g = torch.Generator().manual_seed(cfg.seed)
+    key = cfg.name.split()[0]
+    if key in ("plumbing", "causal-gqa"):
+        q, k, v = (_normal(g, s) for s in (cfg.shape_q, cfg.shape_kv, cfg.shape_kv))
+    elif key == "flux":
+        q, k, v = (_normal(g, s) for s in (cfg.shape_q, cfg.shape_kv, cfg.shape_kv))
+        ch = torch.randperm(cfg.D, generator=g)[:8]
+        k[..., ch] += _normal(g, (8,), math.sqrt(3.0))
+    elif key == "wan14b":
+        q, k, v = (_normal(g, s) for s in (cfg.shape_q, cfg.shape_kv, cfg.shape_kv))
+        n = math.ceil(0.02 * cfg.D)
+        k[..., torch.randperm(cfg.D, generator=g)[:n]] *= 10.0
+        v[..., torch.randperm(cfg.D, generator=g)[:n]] *= 10.0
+    elif key == "hunyuan":
+        q, k, v = (_normal(g, s, 0.5) for s in (cfg.shape_q, cfg.shape_kv, cfg.shape_kv))
+        k += _normal(g, (cfg.D,), math.sqrt(2.0))
+    else:
+        raise KeyError(cfg.name)
+    q, k, v = (t.to(cfg.dtype) for t in (q, k, v))
+    if heads is not None:
+        grp = cfg.H // cfg.Hkv
+        k, v = k[:, heads], v[:, heads]
+        q = q[:, heads.start * grp: heads.stop * grp]
+    return q, k, v

@@ -1,0 +1,73 @@
+// C ABI glue: error reporting, queries and the one-call forward (v_amax -> quant_q -> quant_kv -> attention).
+#include <stdio.h>
+#include <string.h>
+
+#include "sage_host.h"
+
+namespace sage {
+
+static thread_local char g_err[512] = {0};
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+  snprintf(g_err, sizeof(g_err), "%s failed: %s (%d)", what, hipGetErrorString(err), (int)err);
+  return SAGE_ERR_HIP;
+}
+
+void clear_error() { g_err[0] = 0; }
+
+int quant_q_impl(const void*, int64_t, int64_t, int64_t, int, int, int, int, int, float, int8_t*, float*, void*);
+int v_amax_impl(const void*, int64_t, int64_t, int64_t, int, int, int, int, int, float*, void*);
+int quant_kv_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, int, int, int, int,
+                  int, const float*, int8_t*, float*, uint8_t*, void*);
+int attn_impl(const int8_t*, const float*, const int8_t*, const float*, const uint8_t*, const float*, void*, int64_t,
+              int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*);
+
+}  // namespace sage
+
+extern "C" {
+
+int sage_abi_version(void) { return 1; }
+
+const char* sage_last_error(void) { return sage::g_err; }
+
+int sage_kv_pad(int skv) { return skv <= 0 ? 0 : sage::kv_pad(skv); }
+
+const char* sage_manifest_json(void) {
+  return "{\"arch\": \"gfx950\", \"head_dims\": [64, 128], \"dtypes\": [\"bf16\", \"f16\"], "
+         "\"kv_block\": 32, \"kv_pad\": 128, "
+         "\"quant_q\": {\"rows_per_block\": 64, \"threads\": 256, \"lanes_per_row\": 4, \"rotation\": \"fwht_f64\"}, "
+         "\"quant_kv\": {\"rows_per_block\": 128, \"threads\": 256}, "
+         "\"v_amax\": {\"rows_per_block\": 256, \"threads\": 256}, "
+         "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": 2, "
+         "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
+         "\"variants\": [\"d64\", \"d128\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}}";
+}
+
+int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
+                 int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb, int64_t oss,
+                 int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float qs_mul,
+                 int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* stream) {
+  sage::clear_error();
+  // validate everything before the first launch so a bad call leaves the stream untouched
+  SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "sage_forward: sizes must be positive");
+  SAGE_REQUIRE(H % Hkv == 0, "sage_forward: heads %d not a multiple of kv heads %d", H, Hkv);
+  if (D != 64 && D != 128) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 128)", D);
+  if (causal && Sq != Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len == kv_len");
+  int rc;
+  if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;
+  if ((rc = sage::quant_q_impl(q, qsb, qss, qsh, B, H, Sq, D, dtype, qs_mul, q8, qs, stream))) return rc;
+  if ((rc = sage::quant_kv_impl(k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, k8, ks, v8t, stream)))
+    return rc;
+  return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype, nullptr,
+                         stream);
+}
+
+}  // extern "C"

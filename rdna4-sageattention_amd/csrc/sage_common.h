@@ -1,0 +1,151 @@
+// Device helpers shared by the gfx950 SageAttention kernels (wave64, CDNA4).
+//
+// Numerics contract (mirrored bit for bit by oracle/sage_oracle.py):
+//  * Hadamard rotation: float64 fast Walsh-Hadamard transform, stage bit 0 first, butterfly (a, b) -> (a + b, a - b),
+//    then one float32 rounding.  The stages commute, so lanes may own any contiguous slice as long as the stage
+//    order is kept.
+//  * x / s with s shared by a whole row or block: r = RN(1 / s) once, then y0 = x * r, e = fma(-y0, s, x),
+//    y = fma(e, r, y0), which equals the IEEE quotient RN(x / s) (Markstein's correction with a correctly rounded
+//    reciprocal; the remainder e is exact because y0 is within one ulp of x / s).
+//  * int8 rounding: trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)) (kernel_build/sage_quant.py:257, :278).
+//  * fp32 -> E4M3FN: round to nearest even with subnormals, inputs already clamped to +-448.
+// Every translation unit is compiled with -ffp-contract=off: the only fused multiply-adds are the explicit ones.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace sage {
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+enum { DT_BF16 = 0, DT_F16 = 1 };
+
+// ---- element <-> float -------------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ float f16_lo(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w & 0xFFFF))); }
+__device__ __forceinline__ float f16_hi(uint32_t w) { return __half2float(__ushort_as_half((unsigned short)(w >> 16))); }
+
+template <int DT> __device__ __forceinline__ float elem_lo(uint32_t w) { return DT == DT_BF16 ? bf16_lo(w) : f16_lo(w); }
+template <int DT> __device__ __forceinline__ float elem_hi(uint32_t w) { return DT == DT_BF16 ? bf16_hi(w) : f16_hi(w); }
+
+// float32 -> bf16 / fp16 bits, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) { return (uint32_t)__half_as_ushort(__float2half_rn(f)); }
+template <int DT> __device__ __forceinline__ uint32_t f32_to_out_bits(float f) {
+  return DT == DT_BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+}
+
+// ---- cross-lane moves -------------------------------------------------------------------------------------------
+// DPP quad_perm selectors: lane i of each quad reads lane sel[i].
+constexpr int DPP_QUAD_XOR1 = 0xB1;  // [1, 0, 3, 2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;  // [2, 3, 0, 1]
+
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL> __device__ __forceinline__ double dpp_f64(double x) {
+  const int lo = __double2loint(x), hi = __double2hiint(x);
+  const int plo = __builtin_amdgcn_update_dpp(0, lo, CTRL, 0xF, 0xF, false);
+  const int phi = __builtin_amdgcn_update_dpp(0, hi, CTRL, 0xF, 0xF, false);
+  return __hiloint2double(phi, plo);
+}
+// value held by lane (lane ^ 32)
+__device__ __forceinline__ float xor32_f32(float x) {
+  const int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(((lane ^ 32) << 2), __float_as_int(x)));
+}
+
+// ---- Hadamard (float64 FWHT) -----------------------------------------------------------------------------------
+// x holds EPL consecutive elements of a row whose other slices sit in the 1 / 2 / 4 neighbouring lanes of a quad
+// (LANES = D / EPL lanes per row, aligned to quads).  In-lane stages first, then the cross-lane stages, so the
+// global stage order is bit 0, 1, 2, ...
+template <int EPL, int LANES>
+__device__ __forceinline__ void fwht_f64(double (&x)[EPL], int quad_lane) {
+#pragma unroll
+  for (int s = 1; s < EPL; s <<= 1) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      if (!(i & s)) {
+        const double a = x[i], b = x[i + s];
+        x[i] = a + b;
+        x[i + s] = a - b;
+      }
+    }
+  }
+  if (LANES >= 2) {
+    // the lane with the stage bit clear holds a and computes a + b; the other holds b and computes a - b
+    const double sg = (quad_lane & 1) ? -1.0 : 1.0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) x[i] = __builtin_fma(sg, x[i], dpp_f64<DPP_QUAD_XOR1>(x[i]));
+  }
+  if (LANES >= 4) {
+    const double sg = (quad_lane & 2) ? -1.0 : 1.0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) x[i] = __builtin_fma(sg, x[i], dpp_f64<DPP_QUAD_XOR2>(x[i]));
+  }
+}
+
+// max over the LANES lanes of a quad-aligned row group
+template <int LANES> __device__ __forceinline__ float row_max(float v) {
+  if (LANES >= 2) v = fmaxf(v, dpp_f32<DPP_QUAD_XOR1>(v));
+  if (LANES >= 4) v = fmaxf(v, dpp_f32<DPP_QUAD_XOR2>(v));
+  return v;
+}
+
+// ---- quantization helpers ---------------------------------------------------------------------------------------
+// RN(x / s) given r = RN(1 / s)
+__device__ __forceinline__ float div_by_scale(float x, float s, float r) {
+  const float y0 = x * r;
+  const float e = __builtin_fmaf(-y0, s, x);
+  return __builtin_fmaf(e, r, y0);
+}
+
+__device__ __forceinline__ int round_half_away(float y) {
+  const float t = y >= 0.0f ? y + 0.5f : y - 0.5f;
+  return (int)t;  // v_cvt_i32_f32 truncates toward zero
+}
+
+// float32 in [-448, 448] -> E4M3FN byte, round to nearest even, subnormals kept
+__device__ __forceinline__ uint32_t f32_to_e4m3(float y) {
+  const uint32_t u = __float_as_uint(y);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = fabsf(y);
+  uint32_t code;
+  if (a >= 0.015625f) {  // 2^-6, smallest normal E4M3
+    const uint32_t ab = __float_as_uint(a);
+    const uint32_t r = (ab + 0x7FFFFu + ((ab >> 20) & 1u)) >> 20;
+    code = r - ((127u - 7u) << 3);
+  } else {
+    code = (uint32_t)__builtin_rintf(a * 512.0f);  // m * 2^-9, m in 0..8 (8 is the smallest normal code)
+  }
+  return code | sign;
+}
+
+// ---- misc -------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);
+}
+
+// Map a hardware workgroup id to a logical one so that a contiguous logical range lands on one XCD.  Workgroups are
+// dispatched round-robin over the 8 XCDs; XCD x receives ids x, x + 8, x + 16, ...
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+  constexpr int NX = 8;
+  const int q = total / NX, r = total % NX;
+  const int x = id % NX, i = id / NX;
+  return x * q + (x < r ? x : r) + i;
+}
+
+}  // namespace sage

@@ -1,0 +1,41 @@
+// Host-side helpers shared by the C-ABI entry points: error reporting and argument checks.
+// Nothing here touches the GPU, so argument validation works (and is tested) on machines without one.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+
+#include "../../include/sage_capi.h"
+
+namespace sage {
+
+// thread-local message behind sage_last_error(); returns `code` for convenient `return fail(...)`
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t err, const char* what);
+void clear_error();
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+#define SAGE_REQUIRE(cond, ...)                                   \
+  do {                                                            \
+    if (!(cond)) return ::sage::fail(SAGE_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define SAGE_HIP_CHECK(expr, what)                               \
+  do {                                                           \
+    hipError_t _e = (expr);                                      \
+    if (_e != hipSuccess) return ::sage::hip_fail(_e, what);     \
+  } while (0)
+
+// after a kernel launch: report launch-configuration errors without synchronising
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, what);
+  return SAGE_OK;
+}
+
+// padded KV length used by every K8 / KS / V8T layout
+inline int kv_pad(int skv) { return (skv + SAGE_KV_PAD - 1) / SAGE_KV_PAD * SAGE_KV_PAD; }
+
+}  // namespace sage

@@ -1,0 +1,359 @@
+// Quantization kernels of the gfx950 SageAttention path (HBM-bound streaming kernels).
+//
+//  quant_q_kernel   Q rows -> Hadamard (float64 FWHT) -> int8, one scale per token   (sage_quant.py:246-261)
+//  fill_kernel      clears the V amax buffer (a kernel, not hipMemsetAsync, so the sequence can be graph-captured)
+//  v_amax_kernel    per-channel max |v| over a chunk of rows, combined with atomicMax on the fp32 bit pattern
+//                   (values are >= 0, so unsigned order == float order)               (_attention.py:120-121)
+//  quant_kv_kernel  K rows -> Hadamard -> int8, one scale per 32 keys; V -> E4M3 with the per-channel scale,
+//                   transposed through LDS into V8T                                  (sage_quant.py:264-283)
+//
+// Row mapping of the Hadamard kernels: 4 lanes (one quad) per row, each lane owns D / 4 consecutive elements
+// (64 or 32 bytes of bf16 / fp16), so a wave64 rotates 16 rows at a time.
+#include "sage_common.h"
+#include "sage_host.h"
+
+namespace sage {
+
+constexpr int QUAD = 4;
+
+// Load EPL consecutive 16-bit elements (EPL * 2 bytes, 16-byte aligned) and widen them to float64.
+template <int EPL, int DT>
+__device__ __forceinline__ void load_row_slice(const uint16_t* __restrict__ src, bool valid, double (&x)[EPL]) {
+#pragma unroll
+  for (int k = 0; k < EPL / 8; ++k) {
+    uint4 w = valid ? *reinterpret_cast<const uint4*>(src + 8 * k) : make_uint4(0, 0, 0, 0);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[8 * k + 2 * i] = (double)elem_lo<DT>(ws[i]);
+      x[8 * k + 2 * i + 1] = (double)elem_hi<DT>(ws[i]);
+    }
+  }
+}
+
+// Quantize EPL rotated values with the shared scale s (reciprocal r) and store them as EPL int8 bytes.
+template <int EPL>
+__device__ __forceinline__ void quantize_store_i8(const float (&x)[EPL], float s, float r, int8_t* __restrict__ dst,
+                                                  bool valid) {
+  uint32_t words[EPL / 4];
+#pragma unroll
+  for (int i = 0; i < EPL / 4; ++i) {
+    const int a = round_half_away(div_by_scale(x[4 * i + 0], s, r));
+    const int b = round_half_away(div_by_scale(x[4 * i + 1], s, r));
+    const int c = round_half_away(div_by_scale(x[4 * i + 2], s, r));
+    const int d = round_half_away(div_by_scale(x[4 * i + 3], s, r));
+    words[i] = pack4_i8(a, b, c, d);
+  }
+  if (valid) {
+#pragma unroll
+    for (int i = 0; i < EPL / 16; ++i)
+      reinterpret_cast<uint4*>(dst)[i] = make_uint4(words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// quant_q: grid = (ceil(S / 64) * B * H), block = 256 (4 waves x 16 rows)
+// ------------------------------------------------------------------------------------------------------------------
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
+                                                      int64_t sh, int H, int S, int row_tiles, float qs_mul,
+                                                      int8_t* __restrict__ q8, float* __restrict__ qs) {
+  constexpr int EPL = D / QUAD;
+  const int tile = blockIdx.x % row_tiles;
+  const int bh = blockIdx.x / row_tiles;
+  const int b = bh / H, h = bh % H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 3;
+  const int row = tile * 64 + wave * 16 + (lane >> 2);
+  const bool valid = row < S;
+  const uint16_t* src = x + b * sb + (int64_t)(valid ? row : 0) * ss + h * sh + j * EPL;
+
+  double xd[EPL];
+  load_row_slice<EPL, DT>(src, valid, xd);
+  fwht_f64<EPL, QUAD>(xd, j);
+  float xf[EPL];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    xf[i] = (float)xd[i];
+    amax = fmaxf(amax, fabsf(xf[i]));
+  }
+  amax = fmaxf(row_max<QUAD>(amax), 1e-12f);
+  const float s = amax / 127.0f;
+  const float r = 1.0f / s;
+  int8_t* dst = q8 + ((int64_t)bh * S + row) * D + j * EPL;
+  quantize_store_i8<EPL>(xf, s, r, dst, valid);
+  if (valid && j == 0) qs[(int64_t)bh * S + row] = (s / (float)D) * qs_mul;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// fill / v_amax
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ p, int64_t n, float value) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = value;
+}
+
+// grid = (chunks * B * Hkv), block = 256; each block reduces `chunk_rows` rows of one (batch, kv head)
+template <int D, int DT>
+__global__ __launch_bounds__(256) void v_amax_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t ss,
+                                                     int64_t sh, int Hkv, int S, int chunks, int chunk_rows,
+                                                     float* __restrict__ vs) {
+  constexpr int LPR = D / 8;      // lanes per row, 8 elements (16 bytes) each
+  constexpr int RPI = 256 / LPR;  // rows per iteration
+  __shared__ float red[RPI][D + 1];
+  const int chunk = blockIdx.x % chunks;
+  const int bh = blockIdx.x / chunks;
+  const int b = bh / Hkv, h = bh % Hkv;
+  const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
+  const int row_end = min(S, (chunk + 1) * chunk_rows);
+  const uint16_t* base = v + b * sb + h * sh + c8 * 8;
+  float m[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m[i] = 0.0f;
+  for (int row = chunk * chunk_rows + r0; row < row_end; row += RPI) {
+    const uint4 w = *reinterpret_cast<const uint4*>(base + (int64_t)row * ss);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m[2 * i] = fmaxf(m[2 * i], fabsf(elem_lo<DT>(ws[i])));
+      m[2 * i + 1] = fmaxf(m[2 * i + 1], fabsf(elem_hi<DT>(ws[i])));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[r0][c8 * 8 + i] = m[i];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float a = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < RPI; ++r) a = fmaxf(a, red[r][threadIdx.x]);
+    atomicMax(reinterpret_cast<unsigned int*>(vs + (int64_t)bh * D + threadIdx.x), __float_as_uint(a));
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// quant_kv: grid = (Skp / 128 * B * Hkv), block = 256.  Wave w quantizes K rows [32w, 32w + 32) of the block (one K
+// scale) in two passes of 16 rows; then the block converts its 128 V rows to E4M3 and writes them transposed.
+// ------------------------------------------------------------------------------------------------------------------
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss,
+                                                       int64_t ksh, const uint16_t* __restrict__ v, int64_t vsb,
+                                                       int64_t vss, int64_t vsh, int Hkv, int S, int Skp,
+                                                       const float* __restrict__ vs, int8_t* __restrict__ k8,
+                                                       float* __restrict__ ks, uint8_t* __restrict__ v8t) {
+  constexpr int EPL = D / QUAD;
+  constexpr int PITCH = D + 4;  // LDS row pitch of the [128 keys][D] E4M3 staging tile
+  __shared__ uint8_t vtile[128 * PITCH];
+  const int nblk = Skp / 128;
+  const int blk = blockIdx.x % nblk;
+  const int bh = blockIdx.x / nblk;
+  const int b = bh / Hkv, h = bh % Hkv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 3;
+
+  // ---- K ----
+  float xf[2][EPL];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = blk * 128 + wave * 32 + p * 16 + (lane >> 2);
+    const bool valid = row < S;
+    const uint16_t* src = k + b * ksb + (int64_t)(valid ? row : 0) * kss + h * ksh + j * EPL;
+    double xd[EPL];
+    load_row_slice<EPL, DT>(src, valid, xd);
+    fwht_f64<EPL, QUAD>(xd, j);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      xf[p][i] = (float)xd[i];
+      amax = fmaxf(amax, fabsf(xf[p][i]));
+    }
+  }
+  // max over the wave's 32 rows (64 lanes)
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  amax = fmaxf(amax, 1e-12f);
+  const float s = amax / 127.0f;
+  const float r = 1.0f / s;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = blk * 128 + wave * 32 + p * 16 + (lane >> 2);
+    int8_t* dst = k8 + ((int64_t)bh * Skp + row) * D + j * EPL;
+    quantize_store_i8<EPL>(xf[p], s, r, dst, true);
+  }
+  if (lane == 0) ks[(int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 4 + wave] = s;
+
+  // ---- V: scale, E4M3, stage [key][d] in LDS ----
+  constexpr int LPR = D / 8;      // lanes per row (8 channels each)
+  constexpr int RPI = 256 / LPR;  // rows per pass
+  const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
+  float cs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cs[i] = 448.0f / fmaxf(vs[(int64_t)bh * D + c8 * 8 + i], 1e-30f);
+  const uint16_t* vbase = v + b * vsb + h * vsh + c8 * 8;
+#pragma unroll 2
+  for (int rr = r0; rr < 128; rr += RPI) {
+    const int row = blk * 128 + rr;
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (row < S) w = *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t e[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = fminf(fmaxf(elem_lo<DT>(ws[i]) * cs[2 * i], -448.0f), 448.0f);
+      const float hi = fminf(fmaxf(elem_hi<DT>(ws[i]) * cs[2 * i + 1], -448.0f), 448.0f);
+      e[2 * i] = f32_to_e4m3(lo);
+      e[2 * i + 1] = f32_to_e4m3(hi);
+    }
+    uint32_t* t = reinterpret_cast<uint32_t*>(vtile + rr * PITCH + c8 * 8);
+    t[0] = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
+    t[1] = e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24);
+  }
+  __syncthreads();
+
+  // ---- V: transposed store.  Thread -> (4-channel group cg, 16-key set ksel); key set ksel = 4G + u covers output
+  // positions [64G + 16u, +16) of this 128-key block, i.e. keys 64G + 8g + 4h + r with h = u / 2, g = 4(u % 2) + i.
+  constexpr int NCG = D / 4;
+  for (int item = threadIdx.x; item < NCG * 8; item += 256) {
+    const int ksel = item % 8, cg = item / 8;
+    const int G = ksel >> 2, u = ksel & 3, hh = u >> 1;
+    uint32_t wd[4][4];  // [chunk i][key r] -> 4 channel bytes
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int g = 4 * (u & 1) + i;
+#pragma unroll
+      for (int rk = 0; rk < 4; ++rk) {
+        const int key = 64 * G + 8 * g + 4 * hh + rk;
+        wd[i][rk] = *reinterpret_cast<const uint32_t*>(vtile + key * PITCH + cg * 4);
+      }
+    }
+#pragma unroll
+    for (int ci = 0; ci < 4; ++ci) {
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] = ((wd[i][0] >> (8 * ci)) & 0xFFu) | (((wd[i][1] >> (8 * ci)) & 0xFFu) << 8) |
+               (((wd[i][2] >> (8 * ci)) & 0xFFu) << 16) | (((wd[i][3] >> (8 * ci)) & 0xFFu) << 24);
+      }
+      const int d = cg * 4 + ci;
+      uint8_t* dst = v8t + ((int64_t)bh * D + d) * Skp + blk * 128 + 64 * G + 16 * u;
+      *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// launchers
+// ------------------------------------------------------------------------------------------------------------------
+static int check_common(int B, int H, int S, int D, int dtype, const char* who) {
+  SAGE_REQUIRE(B > 0 && H > 0 && S > 0, "%s: sizes must be positive (B=%d H=%d S=%d)", who, B, H, S);
+  if (D != 64 && D != 128) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 128)", who, D);
+  if (dtype != SAGE_DTYPE_BF16 && dtype != SAGE_DTYPE_F16)
+    return fail(SAGE_ERR_UNSUPPORTED, "%s: dtype code %d (bf16=0, f16=1)", who, dtype);
+  return SAGE_OK;
+}
+
+static int check_strided(const void* p, int64_t sb, int64_t ss, int64_t sh, const char* who, const char* name) {
+  SAGE_REQUIRE(p != nullptr, "%s: %s is NULL", who, name);
+  SAGE_REQUIRE(aligned16(p), "%s: %s is not 16-byte aligned", who, name);
+  SAGE_REQUIRE(sb % 8 == 0 && ss % 8 == 0 && sh % 8 == 0 && sb >= 0 && ss >= 0 && sh >= 0,
+               "%s: %s strides (%lld, %lld, %lld) must be non-negative multiples of 8 elements", who, name,
+               (long long)sb, (long long)ss, (long long)sh);
+  return SAGE_OK;
+}
+
+template <int D, int DT>
+static void launch_quant_q(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H, int S, float qs_mul,
+                           int8_t* q8, float* qs, hipStream_t st) {
+  const int tiles = (S + 63) / 64;
+  hipLaunchKernelGGL((quant_q_kernel<D, DT>), dim3(tiles * B * H), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(q), sb, ss, sh, H, S, tiles, qs_mul, q8, qs);
+}
+
+template <int D, int DT>
+static void launch_v_amax(const void* v, int64_t sb, int64_t ss, int64_t sh, int B, int Hkv, int S, float* vs,
+                          hipStream_t st) {
+  const int64_t n = (int64_t)B * Hkv * D;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, vs, n, 0.0f);
+  // aim for ~256 rows per block, but keep the block count per (b, h) bounded
+  int chunk_rows = 256;
+  int chunks = (S + chunk_rows - 1) / chunk_rows;
+  hipLaunchKernelGGL((v_amax_kernel<D, DT>), dim3(chunks * B * Hkv), dim3(256), 0, st, static_cast<const uint16_t*>(v),
+                     sb, ss, sh, Hkv, S, chunks, chunk_rows, vs);
+}
+
+template <int D, int DT>
+static void launch_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const void* v, int64_t vsb,
+                            int64_t vss, int64_t vsh, int B, int Hkv, int S, const float* vs, int8_t* k8, float* ks,
+                            uint8_t* v8t, hipStream_t st) {
+  const int Skp = kv_pad(S);
+  hipLaunchKernelGGL((quant_kv_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(k), ksb, kss, ksh, static_cast<const uint16_t*>(v), vsb, vss, vsh,
+                     Hkv, S, Skp, vs, k8, ks, v8t);
+}
+
+#define SAGE_DISPATCH_D_DT(D, DT, FN, ...)                                      \
+  do {                                                                        \
+    if ((D) == 64 && (DT) == SAGE_DTYPE_BF16) FN<64, DT_BF16>(__VA_ARGS__);    \
+    else if ((D) == 64) FN<64, DT_F16>(__VA_ARGS__);                            \
+    else if ((DT) == SAGE_DTYPE_BF16) FN<128, DT_BF16>(__VA_ARGS__);           \
+    else FN<128, DT_F16>(__VA_ARGS__);                                        \
+  } while (0)
+
+int quant_q_impl(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H, int Sq, int D, int dtype,
+                 float qs_mul, int8_t* q8, float* qs, void* stream) {
+  const char* who = "sage_quant_q";
+  int rc = check_common(B, H, Sq, D, dtype, who);
+  if (rc) return rc;
+  if ((rc = check_strided(q, sb, ss, sh, who, "q"))) return rc;
+  SAGE_REQUIRE(q8 != nullptr && qs != nullptr, "%s: q8 / qs is NULL", who);
+  SAGE_REQUIRE(aligned16(q8), "%s: q8 is not 16-byte aligned", who);
+  SAGE_DISPATCH_D_DT(D, dtype, launch_quant_q, q, sb, ss, sh, B, H, Sq, qs_mul, q8, qs, (hipStream_t)stream);
+  return check_launch("quant_q launch");
+}
+
+int v_amax_impl(const void* v, int64_t sb, int64_t ss, int64_t sh, int B, int Hkv, int Skv, int D, int dtype,
+                float* vs, void* stream) {
+  const char* who = "sage_v_amax";
+  int rc = check_common(B, Hkv, Skv, D, dtype, who);
+  if (rc) return rc;
+  if ((rc = check_strided(v, sb, ss, sh, who, "v"))) return rc;
+  SAGE_REQUIRE(vs != nullptr, "%s: vs is NULL", who);
+  SAGE_DISPATCH_D_DT(D, dtype, launch_v_amax, v, sb, ss, sh, B, Hkv, Skv, vs, (hipStream_t)stream);
+  return check_launch("v_amax launch");
+}
+
+int quant_kv_impl(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss,
+                  int64_t vsh, int B, int Hkv, int Skv, int D, int dtype, const float* vs, int8_t* k8, float* ks,
+                  uint8_t* v8t, void* stream) {
+  const char* who = "sage_quant_kv";
+  int rc = check_common(B, Hkv, Skv, D, dtype, who);
+  if (rc) return rc;
+  if ((rc = check_strided(k, ksb, kss, ksh, who, "k"))) return rc;
+  if ((rc = check_strided(v, vsb, vss, vsh, who, "v"))) return rc;
+  SAGE_REQUIRE(vs != nullptr && k8 != nullptr && ks != nullptr && v8t != nullptr, "%s: an output pointer is NULL", who);
+  SAGE_REQUIRE(aligned16(k8) && aligned16(v8t), "%s: k8 / v8t must be 16-byte aligned", who);
+  SAGE_DISPATCH_D_DT(D, dtype, launch_quant_kv, k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, vs, k8, ks, v8t,
+                     (hipStream_t)stream);
+  return check_launch("quant_kv launch");
+}
+
+}  // namespace sage
+
+extern "C" int sage_quant_q(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H, int Sq, int D, int dtype,
+                            float qs_mul, int8_t* q8, float* qs, void* stream) {
+  sage::clear_error();
+  return sage::quant_q_impl(q, sb, ss, sh, B, H, Sq, D, dtype, qs_mul, q8, qs, stream);
+}
+
+extern "C" int sage_v_amax(const void* v, int64_t sb, int64_t ss, int64_t sh, int B, int Hkv, int Skv, int D, int dtype,
+                           float* vs, void* stream) {
+  sage::clear_error();
+  return sage::v_amax_impl(v, sb, ss, sh, B, Hkv, Skv, D, dtype, vs, stream);
+}
+
+extern "C" int sage_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const void* v, int64_t vsb,
+                             int64_t vss, int64_t vsh, int B, int Hkv, int Skv, int D, int dtype, const float* vs,
+                             int8_t* k8, float* ks, uint8_t* v8t, void* stream) {
+  sage::clear_error();
+  return sage::quant_kv_impl(k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, k8, ks, v8t, stream);
+}

@@ -1,0 +1,140 @@
+"""SageAttention 2.2 API on top of cdna4_sage (AMD MI355X, gfx950).
+
+Every public function of SageAttention 2.2 keeps its signature (reference: src/sageattention/core.py:60-142).  All of
+them run the same path (Hadamard-rotated int8 Q K^T, fp8 P V with per-channel V scales); kernel-selection arguments
+such as qk_quant_gran, pv_accum_dtype, smooth_k, smooth_v or value_dtype are accepted and ignored.  Calls the gfx950
+kernels cannot run or would not win on (masks, small problems, unsupported head dims or GPUs) use torch SDPA, so the
+functions work on any device torch supports.
+"""
+from typing import Any, Optional
+
+import torch
+
+import cdna4_sage
+
+_LSE_SCORE_BUDGET = 64 * 2**20  # fp32 scores per chunk of the LSE pass (~256 MB)
+
+
+def _as_hnd(t: torch.Tensor, tensor_layout: str) -> torch.Tensor:
+    if tensor_layout == "HND":
+        return t
+    if tensor_layout == "NHD":
+        return t.transpose(1, 2)
+    raise ValueError(f"tensor_layout must be 'HND' or 'NHD', got {tensor_layout!r}")
+
+
+def _lse(q, k, tensor_layout, is_causal, sm_scale):
+    """Row logsumexp of Q K^T * scale over the keys, fp32 [B, H, q_len], on the unquantized inputs
+    (reference: src/sageattention/core.py:36-57).  Causal masks are bottom-right aligned.  The query heads that share
+    a kv head are processed together with one fp32 batched product per row chunk."""
+    q, k = _as_hnd(q, tensor_layout), _as_hnd(k, tensor_layout)
+    B, H, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    rep = H // Hkv
+    scale = D ** -0.5 if sm_scale is None else sm_scale
+    out = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
+    rows = max(1, _LSE_SCORE_BUDGET // max(1, Skv * rep))
+    key_idx = torch.arange(Skv, device=q.device)
+    for b in range(B):
+        for g in range(Hkv):
+            kt = k[b, g].float().t().contiguous()                       # [D, Skv]
+            qg = q[b, g * rep:(g + 1) * rep]                             # [rep, Sq, D]
+            for r0 in range(0, Sq, rows):
+                r1 = min(Sq, r0 + rows)
+                sc = torch.matmul(qg[:, r0:r1].float(), kt) * scale      # [rep, rows, Skv]
+                if is_causal:
+                    last = torch.arange(r0, r1, device=q.device) + (Skv - Sq)
+                    sc.masked_fill_(key_idx[None, None, :] > last[None, :, None], float("-inf"))
+                out[b, g * rep:(g + 1) * rep, r0:r1] = torch.logsumexp(sc, dim=-1)
+    return out
+
+
+def sageattn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    tensor_layout: str = "HND",
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    return_lse: bool = False,
+    **kwargs: Any,
+):
+    """Attention for [B, H, L, D] ("HND") or [B, L, H, D] ("NHD") fp16 / bf16 tensors; returns the input layout and
+    dtype, plus the row logsumexp [B, H, q_len] when return_lse is True.  Causal masks are bottom-right aligned.
+    There is no attn_mask parameter (ComfyUI reads the signature); a mask passed as a keyword goes to SDPA."""
+    out = cdna4_sage.sageattn(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal, sm_scale=sm_scale,
+                              attn_mask=kwargs.get("attn_mask"))
+    if return_lse:
+        return out, _lse(q, k, tensor_layout, is_causal, sm_scale)
+    return out
+
+
+def sageattn_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    is_causal: bool = False,
+    sm_scale: Optional[float] = None,
+    smooth_k: bool = True,
+    **kwargs: Any,
+) -> torch.Tensor:
+    """Packed variable-length attention: q [total_q, H, D], k / v [total_k, Hkv, D], cu_seqlens [batch + 1]
+    (reference: src/sageattention/core.py:79-102).  Each sequence is routed like a sageattn call; empty query
+    sequences are skipped."""
+    bq = [int(x) for x in cu_seqlens_q.tolist()]
+    bk = [int(x) for x in cu_seqlens_k.tolist()]
+    out = torch.empty_like(q)
+    for (q0, q1), (k0, k1) in zip(zip(bq[:-1], bq[1:]), zip(bk[:-1], bk[1:])):
+        if q1 == q0:
+            continue
+        o = sageattn(q[q0:q1].unsqueeze(0), k[k0:k1].unsqueeze(0), v[k0:k1].unsqueeze(0), tensor_layout="NHD",
+                     is_causal=is_causal, sm_scale=sm_scale)
+        out[q0:q1] = o[0]
+    return out
+
+
+def _variant(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, return_lse=False, **kwargs):
+    return sageattn(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal, sm_scale=sm_scale,
+                    return_lse=return_lse, attn_mask=kwargs.get("attn_mask"))
+
+
+def sageattn_qk_int8_pv_fp16_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                    quantization_backend: str = "triton", is_causal: bool = False,
+                                    attn_mask: Optional[torch.Tensor] = None, sm_scale: Optional[float] = None,
+                                    smooth_k: bool = True, return_lse: bool = False, **kwargs: Any):
+    return _variant(q, k, v, tensor_layout, is_causal, sm_scale, return_lse, attn_mask=attn_mask)
+
+
+def sageattn_qk_int8_pv_fp16_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                  is_causal: bool = False, qk_quant_gran: str = "per_thread",
+                                  sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32",
+                                  smooth_k: bool = True, smooth_v: bool = False, return_lse: bool = False,
+                                  **kwargs: Any):
+    return _variant(q, k, v, tensor_layout, is_causal, sm_scale, return_lse)
+
+
+def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                 is_causal: bool = False, qk_quant_gran: str = "per_thread",
+                                 sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32+fp16",
+                                 smooth_k: bool = True, smooth_v: bool = False, return_lse: bool = False,
+                                 **kwargs: Any):
+    return _variant(q, k, v, tensor_layout, is_causal, sm_scale, return_lse)
+
+
+def sageattn_qk_int8_pv_fp8_cuda_sm90(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                      is_causal: bool = False, qk_quant_gran: str = "per_thread",
+                                      sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32+fp32",
+                                      smooth_k: bool = True, return_lse: bool = False, **kwargs: Any):
+    return _variant(q, k, v, tensor_layout, is_causal, sm_scale, return_lse)
+
+
+def sageattn_qk_int8_pv_gfx12_native(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                     is_causal: bool = False, qk_quant_gran: str = "per_warp",
+                                     sm_scale: Optional[float] = None, pv_accum_dtype: Optional[str] = None,
+                                     value_dtype: str = "fp8", smooth_k: bool = True, smooth_v: bool = False,
+                                     return_lse: bool = False, **kwargs: Any):
+    return _variant(q, k, v, tensor_layout, is_causal, sm_scale, return_lse)

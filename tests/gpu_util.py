@@ -1,0 +1,66 @@
+"""Helpers of the GPU parity tests: run each C-ABI entry point on device tensors and bring the results back."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from cdna4_sage import _capi
+
+DT = {torch.bfloat16: _capi.DTYPE_BF16, torch.float16: _capi.DTYPE_F16}
+
+
+def bsh(t: torch.Tensor, layout: str):
+    return (t.stride(0), t.stride(2), t.stride(1)) if layout == "HND" else (t.stride(0), t.stride(1), t.stride(2))
+
+
+def stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def run_quant_q(q: torch.Tensor, layout="HND", qs_mul=1.0):
+    dev = q.device
+    if layout == "HND":
+        B, H, S, D = q.shape
+    else:
+        B, S, H, D = q.shape
+    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
+    qs = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    _capi.call("sage_quant_q", q.data_ptr(), *bsh(q, layout), B, H, S, D, DT[q.dtype], qs_mul, q8.data_ptr(),
+               qs.data_ptr(), stream(dev))
+    torch.cuda.synchronize(dev)
+    return q8.cpu().numpy(), qs.cpu().numpy()
+
+
+def run_quant_kv(k: torch.Tensor, v: torch.Tensor, layout="HND"):
+    dev = k.device
+    if layout == "HND":
+        B, Hkv, S, D = k.shape
+    else:
+        B, S, Hkv, D = k.shape
+    skp = _capi.kv_pad(S)
+    vs = torch.empty(B, Hkv, D, dtype=torch.float32, device=dev)
+    k8 = torch.empty(B, Hkv, skp, D, dtype=torch.int8, device=dev)
+    ks = torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev)
+    v8t = torch.empty(B, Hkv, D, skp, dtype=torch.uint8, device=dev)
+    st = stream(dev)
+    _capi.call("sage_v_amax", v.data_ptr(), *bsh(v, layout), B, Hkv, S, D, DT[v.dtype], vs.data_ptr(), st)
+    _capi.call("sage_quant_kv", k.data_ptr(), *bsh(k, layout), v.data_ptr(), *bsh(v, layout), B, Hkv, S, D,
+               DT[k.dtype], vs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(), st)
+    torch.cuda.synchronize(dev)
+    return k8.cpu().numpy(), ks.cpu().numpy(), v8t.cpu().numpy(), vs.cpu().numpy()
+
+
+def hnd_np(t: torch.Tensor, layout="HND") -> np.ndarray:
+    """float32 numpy copy in HND layout."""
+    t = t if layout == "HND" else t.transpose(1, 2)
+    return t.float().cpu().numpy()
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def cosine(a, b) -> float:
+    a = np.asarray(a, dtype=np.float64).ravel()
+    b = np.asarray(b, dtype=np.float64).ravel()
+    return float((a * b).sum() / np.sqrt((a * a).sum() * (b * b).sum()))

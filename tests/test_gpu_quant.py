@@ -1,0 +1,97 @@
+"""Bit-exact parity of the gfx950 quantizers with the CPU oracle (int8 Q/K, E4M3 V and every scale)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits, hnd_np, run_quant_kv, run_quant_q
+from oracle import sage_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+Q_CASES = [  # B, H, S, D, dtype, layout
+    (1, 2, 100, 128, torch.bfloat16, "HND"),
+    (2, 3, 777, 64, torch.float16, "NHD"),
+    (1, 4, 1, 128, torch.bfloat16, "HND"),
+    (1, 2, 4099, 64, torch.bfloat16, "NHD"),
+    (2, 5, 130, 128, torch.float16, "HND"),
+    (1, 24, 4608, 128, torch.bfloat16, "HND"),   # config 2 (Flux) at full size
+]
+
+
+def _randn(shape, dtype, seed, layout="HND", scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    B, H, S, D = shape
+    t = torch.randn(B, H, S, D, generator=g) * scale
+    t = t.to(dtype)
+    return t if layout == "HND" else t.transpose(1, 2).contiguous()
+
+
+@pytest.mark.parametrize("B,H,S,D,dt,layout", Q_CASES)
+def test_quant_q_bitexact(dev, B, H, S, D, dt, layout):
+    q = _randn((B, H, S, D), dt, 11 + S, layout)
+    q8, qs = run_quant_q(q.to(dev), layout)
+    e8, es = orc.quant_q(hnd_np(q, layout))
+    assert np.array_equal(q8, e8), f"Q8 mismatch at {np.argwhere(q8 != e8)[:5]}"
+    assert np.array_equal(bits(qs), bits(es))
+
+
+def test_quant_q_sm_scale_fold(dev):
+    q = _randn((1, 2, 300, 128), torch.bfloat16, 5)
+    f = orc.qs_fold_factor(0.05, 128)
+    _, qs = run_quant_q(q.to(dev), "HND", float(f))
+    _, es = orc.quant_q(hnd_np(q), sm_scale=0.05)
+    assert np.array_equal(bits(qs), bits(es))
+
+
+KV_CASES = [  # B, Hkv, S, D, dtype, layout
+    (1, 2, 100, 128, torch.bfloat16, "HND"),
+    (2, 3, 777, 64, torch.float16, "NHD"),
+    (1, 1, 1, 128, torch.bfloat16, "HND"),
+    (1, 2, 1031, 64, torch.bfloat16, "HND"),
+    (2, 2, 257, 128, torch.float16, "NHD"),
+    (1, 24, 4608, 128, torch.bfloat16, "HND"),   # config 2 (Flux) at full size
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,dt,layout", KV_CASES)
+def test_quant_kv_bitexact(dev, B, H, S, D, dt, layout):
+    k = _randn((B, H, S, D), dt, 21 + S, layout)
+    v = _randn((B, H, S, D), dt, 31 + S, layout, scale=2.0)
+    k8, ks, v8t, vs = run_quant_kv(k.to(dev), v.to(dev), layout)
+    skp = k8.shape[2]
+    e8, eks, ev8, evs = orc.quant_kv(hnd_np(k, layout), hnd_np(v, layout), seq_pad=skp)
+    assert np.array_equal(bits(vs), bits(evs)), "VS mismatch"
+    assert np.array_equal(k8, e8), f"K8 mismatch at {np.argwhere(k8 != e8)[:5]}"
+    assert np.array_equal(bits(ks), bits(eks)), "KS mismatch"
+    ev8t = orc.v8_to_device_layout(ev8)
+    assert np.array_equal(v8t, ev8t), f"V8T mismatch at {np.argwhere(v8t != ev8t)[:5]}"
+
+
+def test_quant_edge_values(dev):
+    """Zero rows, a zero V channel, outlier channels, wide exponent spread and fp16 subnormals."""
+    for dt in (torch.bfloat16, torch.float16):
+        g = torch.Generator().manual_seed(3)
+        S, D = 200, 128
+        k = torch.randn(1, 2, S, D, generator=g)
+        v = torch.randn(1, 2, S, D, generator=g)
+        k[:, :, 5] = 0.0                       # a zero row (scale clamps at 1e-12)
+        k[:, :, 7, 3] = 300.0                  # one outlier
+        k[:, 1, 40:72] = 0.0                   # a whole zero K block
+        v[:, :, :, 9] = 0.0                    # a zero V channel
+        v[:, 0, :, 17] *= 1000.0 if dt == torch.bfloat16 else 100.0
+        k[:, :, 100] *= 1e-3
+        if dt == torch.float16:
+            k[:, :, 120] = torch.randn(1, 2, D, generator=g) * 2.0**-20   # fp16 subnormals
+            v[:, :, 121] = torch.randn(1, 2, D, generator=g) * 2.0**-20
+        else:
+            k[:, :, 120] *= 2.0**-60
+            v[:, :, 121] *= 2.0**-60
+        k, v = k.to(dt), v.to(dt)
+        q8, qs = run_quant_q(k.to(dev))
+        e8, es = orc.quant_q(hnd_np(k))
+        assert np.array_equal(q8, e8) and np.array_equal(bits(qs), bits(es)), dt
+        k8, ks, v8t, vs = run_quant_kv(k.to(dev), v.to(dev))
+        ek8, eks, ev8, evs = orc.quant_kv(hnd_np(k), hnd_np(v), seq_pad=k8.shape[2])
+        assert np.array_equal(k8, ek8) and np.array_equal(bits(ks), bits(eks)), dt
+        assert np.array_equal(bits(vs), bits(evs)), dt
+        assert np.array_equal(v8t, orc.v8_to_device_layout(ev8)), dt
