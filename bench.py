@@ -1,0 +1,239 @@
+"""Benchmark of the MI355X SageAttention path on BASELINE.json's metric configuration.
+
+Workload: config 2, Flux-style joint attention, HND bf16 [1, 24, 4608, 128], non-causal, seeded synthetic inputs
+(K with outlier channels), resident in HBM before the timed region.  One step = one ``sageattention.sageattn`` call,
+i.e. the whole hot path: V amax, Q quantizer, K/V quantizer and the int8/fp8 attention kernel.
+
+Prints ONE JSON line on stdout:
+  value        whole-call throughput in TOPS (algorithmic ops 4*B*H*Sq*Skv*D per call / wall time per call)
+  roofline     the attention kernel (dominant): achieved TFLOP/s from HIP events around back-to-back launches on the
+               launch stream, against MI355X's dense int8/fp8 MFMA peak (5.0 PFLOP/s)
+  cpu_baseline the reference's quantized math (the numpy port in oracle/) timed on this host on a head sample
+Everything else (per-kernel times, quantizer GB/s, torch SDPA bf16 on the same GPU) goes to the "detail" object.
+
+usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--config 2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT / "rdna4-sageattention_amd"), str(ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+MFMA_PEAK_TFLOPS = 5000.0   # MI355X dense int8 / OCP-fp8 MFMA, ops/s / 1e12
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_events(fn, iters):
+    """Average ms per call of fn() launched back to back on torch's current stream, measured with HIP events."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def cpu_baseline(cfg, target_s=15.0):
+    """Time the numpy port of the reference's quantized math on a sample of whole heads (full sequence), as many
+    heads as fit ~target_s of work; report TOPS of the sample.  Also time torch SDPA fp32 on the CPU per head."""
+    import numpy as np
+    import torch
+
+    from cdna4_sage.configs import make_inputs
+    from oracle import sage_oracle as orc
+
+    threads = torch.get_num_threads()
+    grp = cfg.H // cfg.Hkv
+
+    def one(nh):
+        q, k, v = make_inputs(cfg, heads=slice(0, nh))
+        qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+        t0 = time.perf_counter()
+        q8, qs = orc.quant_q(qn)
+        k8, ks, v8, vs = orc.quant_kv(kn, vn)
+        orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=cfg.causal, block_n=32)
+        return time.perf_counter() - t0, (q, k, v)
+
+    t1, _ = one(1)                                   # one kv head (and its query heads) to size the sample
+    nh = int(max(1, min(cfg.Hkv, target_s // max(t1, 1e-3))))
+    if nh > 1:
+        t_emu, (q, k, v) = one(nh)
+    else:
+        t_emu, (q, k, v) = t1, make_inputs(cfg, heads=slice(0, 1))
+    ops = cfg.attention_ops() * nh / cfg.Hkv
+    # torch SDPA fp32 on the CPU, same heads
+    qf, kf, vf = (t.float() for t in (q, k, v))
+    t0 = time.perf_counter()
+    torch.nn.functional.scaled_dot_product_attention(qf, kf.repeat_interleave(grp, 1), vf.repeat_interleave(grp, 1),
+                                                     is_causal=cfg.causal)
+    t_sdpa = time.perf_counter() - t0
+    return {
+        "value": round(ops / t_emu / 1e12, 6),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{nh * grp} of {cfg.H} query heads ({nh} kv heads) of {cfg.name}, full sequence; numpy float32 "
+                  f"emulation of the quantized path (block_n 32), {t_emu:.2f} s; whole call extrapolated "
+                  f"x{cfg.Hkv / nh:.1f} = {t_emu * cfg.Hkv / nh * 1e3:.0f} ms",
+        "sdpa_fp32_cpu_tops": round(ops / t_sdpa / 1e12, 6),
+        "sdpa_fp32_cpu_ms_extrapolated": round(t_sdpa * cfg.Hkv / nh * 1e3, 1),
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-iters", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported (each call is a single-device "
+              "op; multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import torch.nn.functional as F
+
+    import cdna4_sage
+    import sageattention
+    from cdna4_sage import _attention, _capi
+    from cdna4_sage.configs import CONFIGS, make_inputs
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(dev)} arch {_attention.device_arch(dev)}; workload {cfg.name}")
+    q, k, v = (t.to(dev) for t in make_inputs(cfg))
+    torch.cuda.synchronize()
+
+    def step():
+        return sageattention.sageattn(q, k, v, tensor_layout="HND", is_causal=cfg.causal)
+
+    assert cdna4_sage._worth_it(q, k, "HND", cfg.causal), "config must route to the gfx950 kernel"
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ops = cfg.attention_ops()
+    tops = ops / (ms * 1e-3) / 1e12
+
+    # ---- per-kernel times: the same launches the call makes, each looped on torch's current stream ----
+    B, H, Hkv, S, D = cfg.B, cfg.H, cfg.Hkv, cfg.S, cfg.D
+    skp = _capi.kv_pad(S)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
+    qs = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    k8 = torch.empty(B, Hkv, skp, D, dtype=torch.int8, device=dev)
+    ks = torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev)
+    v8t = torch.empty(B, Hkv, D, skp, dtype=torch.uint8, device=dev)
+    vs = torch.empty(B, Hkv, D, dtype=torch.float32, device=dev)
+    out = torch.empty(B, S, H, D, dtype=q.dtype, device=dev)
+    hs = (q.stride(0), q.stride(2), q.stride(1))
+    ks_ = (k.stride(0), k.stride(2), k.stride(1))
+    vs_ = (v.stride(0), v.stride(2), v.stride(1))
+    dt = _capi.DTYPE_BF16 if q.dtype == torch.bfloat16 else _capi.DTYPE_F16
+    L = _capi.lib()
+
+    def k_amax():
+        L.sage_v_amax(v.data_ptr(), *vs_, B, Hkv, S, D, dt, vs.data_ptr(), st)
+
+    def k_q():
+        L.sage_quant_q(q.data_ptr(), *hs, B, H, S, D, dt, 1.0, q8.data_ptr(), qs.data_ptr(), st)
+
+    def k_kv():
+        L.sage_quant_kv(k.data_ptr(), *ks_, v.data_ptr(), *vs_, B, Hkv, S, D, dt, vs.data_ptr(), k8.data_ptr(),
+                        ks.data_ptr(), v8t.data_ptr(), st)
+
+    def k_attn():
+        L.sage_attn_fwd(q8.data_ptr(), qs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(), vs.data_ptr(),
+                        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), B, H, Hkv, S, S, D,
+                        int(cfg.causal), dt, None, st)
+
+    k_amax(); k_q(); k_kv(); k_attn()
+    torch.cuda.synchronize()
+    it = args.kernel_iters
+    t_amax = time_events(k_amax, it)
+    t_q = time_events(k_q, it)
+    t_kv = time_events(k_kv, it)
+    t_attn = time_events(k_attn, it)
+    attn_tflops = ops / (t_attn * 1e-3) / 1e12
+    q_bytes = cfg.quant_q_bytes()
+    kv_bytes = cfg.quant_kv_bytes(skp)
+
+    # ---- torch SDPA bf16 on the same GPU, same method as the step ----
+    sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=cfg.causal)  # noqa: E731
+    for _ in range(args.warmup):
+        sdpa()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sdpa()
+    torch.cuda.synchronize()
+    ms_sdpa = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    result = {
+        "metric": "attention TOPS + ms/call (Flux 24x4608x128), % of int8/fp8 MFMA peak",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 QK / fp8-e4m3 PV (fp32 softmax, bf16 in/out)",
+        "data": "synthetic (seeded, CPU-generated, resident in HBM)",
+        "config": {"workload": cfg.name, "B": B, "H": H, "Hkv": Hkv, "Sq": S, "Skv": S, "D": D,
+                   "layout": "HND", "input_dtype": str(q.dtype).replace("torch.", ""), "causal": cfg.causal},
+        "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(attn_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "attn_kernel<128,false,bf16>", "ms_per_launch": round(t_attn, 5),
+                     "ops_per_launch": ops},
+        "detail": {
+            "call_frac_of_peak": round(tops / MFMA_PEAK_TFLOPS, 4),
+            "kernel_ms": {"v_amax+fill": round(t_amax, 5), "quant_q": round(t_q, 5), "quant_kv": round(t_kv, 5),
+                          "attn": round(t_attn, 5)},
+            "quant_q_GBps": round(q_bytes / (t_q * 1e-3) / 1e9, 1),
+            "quant_kv_GBps": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
+            "hbm_peak_GBps": HBM_PEAK_GBS,
+            "sdpa_bf16_gpu_ms": round(ms_sdpa, 4),
+            "speedup_vs_sdpa_bf16": round(ms_sdpa / ms, 3),
+            "device": torch.cuda.get_device_name(dev),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(cfg)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,177 @@
+"""Host-side behaviour that needs no GPU: API surface, SDPA routing, the torch.library op's fake implementation,
+the return_lse path and varlen, checked against the reference's documented semantics
+(src/sageattention/core.py, src/rdna4_sage/__init__.py, tests/test_sageattention.py)."""
+import inspect
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import cdna4_sage
+import rdna4_sage
+import sageattention
+from oracle import sage_oracle as orc
+
+VARIANTS = ["sageattn_qk_int8_pv_fp16_triton", "sageattn_qk_int8_pv_fp16_cuda", "sageattn_qk_int8_pv_fp8_cuda",
+            "sageattn_qk_int8_pv_fp8_cuda_sm90", "sageattn_qk_int8_pv_gfx12_native"]
+
+
+def _rand(shape, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dtype)
+
+
+def test_api_surface():
+    for n in ["sageattn", "sageattn_varlen"] + VARIANTS:
+        assert callable(getattr(sageattention, n)), n
+    # ComfyUI decides mask support from the signature: SageAttention 2.2's sageattn has no attn_mask parameter
+    assert "attn_mask" not in inspect.signature(sageattention.sageattn).parameters
+    params = {n: list(inspect.signature(getattr(sageattention, n)).parameters) for n in VARIANTS}
+    assert params["sageattn_qk_int8_pv_fp16_triton"][:5] == ["q", "k", "v", "tensor_layout", "quantization_backend"]
+    assert "attn_mask" in params["sageattn_qk_int8_pv_fp16_triton"]
+    assert "qk_quant_gran" in params["sageattn_qk_int8_pv_fp8_cuda"] and "pv_accum_dtype" in params["sageattn_qk_int8_pv_fp8_cuda"]
+    assert "value_dtype" in params["sageattn_qk_int8_pv_gfx12_native"]
+    vp = inspect.signature(sageattention.sageattn_varlen).parameters
+    assert list(vp)[:7] == ["q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q", "max_seqlen_k"]
+    for mod in (cdna4_sage, rdna4_sage):
+        for n in ["sageattn", "attention", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]:
+            assert hasattr(mod, n), (mod, n)
+    assert cdna4_sage.ARCHS == ("gfx950",) and cdna4_sage.HEAD_DIMS == (64, 128)
+    assert hasattr(torch.ops.cdna4_sage, "attention") and hasattr(torch.ops.rdna4_sage, "attention")
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_cpu_tensors_route_to_sdpa(layout, causal):
+    q, k, v = (_rand((1, 4, 300, 64), s, torch.bfloat16) for s in (1, 2, 3))
+    if layout == "NHD":
+        q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    th = (lambda t: t) if layout == "HND" else (lambda t: t.transpose(1, 2))
+    out = sageattention.sageattn(q, k, v, tensor_layout=layout, is_causal=causal)
+    ref = th(F.scaled_dot_product_attention(th(q), th(k), th(v), is_causal=causal))
+    assert out.shape == q.shape and out.dtype == q.dtype
+    torch.testing.assert_close(out, ref, rtol=0, atol=0)
+
+
+def test_kernel_forced_api_raises_unsupported_on_cpu():
+    q = _rand((1, 2, 64, 64), 4, torch.bfloat16)
+    with pytest.raises(cdna4_sage.Unsupported):
+        cdna4_sage.attention(q, q, q, "HND")
+    with pytest.raises(rdna4_sage.Unsupported):
+        rdna4_sage.attention(q, q, q, "HND")
+    with pytest.raises(cdna4_sage.Unsupported, match="layout"):
+        cdna4_sage.check_supported(q, q, q, "BHSD")
+    with pytest.raises(NotImplementedError):
+        cdna4_sage.sageattn(q, q, q, return_lse=True)
+
+
+def test_causal_q_len_ne_kv_len_is_bottom_right():
+    q = _rand((1, 2, 30, 64), 5)
+    k, v = _rand((1, 2, 50, 64), 6), _rand((1, 2, 50, 64), 7)
+    keep = torch.ones(30, 50, dtype=torch.bool).tril(50 - 30)
+    torch.testing.assert_close(sageattention.sageattn(q, k, v, is_causal=True),
+                               F.scaled_dot_product_attention(q, k, v, attn_mask=keep))
+
+
+def test_mask_and_gqa_go_to_sdpa():
+    q = _rand((1, 8, 40, 64), 8)
+    k, v = _rand((1, 2, 40, 64), 9), _rand((1, 2, 40, 64), 10)
+    m = torch.zeros(1, 1, 40, 40)
+    m[..., :5] = float("-inf")
+    ref = F.scaled_dot_product_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), attn_mask=m)
+    torch.testing.assert_close(sageattention.sageattn(q, k, v, attn_mask=m), ref)
+    torch.testing.assert_close(sageattention.sageattn(q, k, v),
+                               F.scaled_dot_product_attention(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1)))
+
+
+def test_worth_it_thresholds_and_env_names():
+    q = torch.empty(1, 24, 4608, 128, device="meta")
+    assert cdna4_sage._worth_it(q, q, "HND")
+    small = torch.empty(1, 8, 1024, 64, device="meta")                # config 1: 8.4 M < 64 Mi -> SDPA
+    assert not cdna4_sage._worth_it(small, small, "HND")
+    short = torch.empty(1, 64, 2048, 64, device="meta")
+    kshort = torch.empty(1, 64, 512, 64, device="meta")              # kv shorter than MIN_KV -> SDPA
+    assert not cdna4_sage._worth_it(short, kshort, "HND")
+    code = "import sys; sys.path.insert(0, sys.argv[1]); import cdna4_sage as c; print(c.MIN_WORK, c.MIN_KV)"
+    pkg = os.path.join(os.path.dirname(__file__), "..", "rdna4-sageattention_amd")
+    for env, want in [({"RDNA4_SAGE_MIN_WORK": "5", "RDNA4_SAGE_MIN_KV": "7"}, "5 7"),
+                      ({"CDNA4_SAGE_MIN_WORK": "9", "RDNA4_SAGE_MIN_WORK": "5"}, "9 1024")]:
+        e = {k: v for k, v in os.environ.items() if "SAGE_MIN" not in k}
+        e.update(env)
+        out = subprocess.run([sys.executable, "-c", code, pkg], env=e, capture_output=True, text=True, check=True)
+        assert out.stdout.strip() == want
+
+
+def test_fake_impl_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(2, 24, 100, 128, dtype=torch.bfloat16)
+        kv = torch.empty(2, 8, 300, 128, dtype=torch.bfloat16)
+        assert torch.ops.cdna4_sage.attention(q, kv, kv, "HND", 0.0, False).shape == (2, 100, 24, 128)
+        qn = torch.empty(2, 100, 24, 64, dtype=torch.float16)
+        kvn = torch.empty(2, 300, 8, 64, dtype=torch.float16)
+        o = torch.ops.rdna4_sage.attention(qn, kvn, kvn, "NHD", 0.0, False)
+        assert o.shape == (2, 100, 24, 64) and o.dtype == torch.float16
+
+
+@pytest.mark.parametrize("layout", ["HND", "NHD"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_return_lse_matches_float64(layout, causal):
+    """LSE semantics of src/sageattention/core.py:36-57 (unquantized fp32, bottom-right causal, GQA) against a
+    float64 logsumexp; the reference's gate is atol 2e-3, rtol 1e-4 (tests/test_sageattention.py:77)."""
+    q = _rand((1, 4, 70, 64), 11, torch.float16)
+    k, v = _rand((1, 2, 90, 64), 12, torch.float16), _rand((1, 2, 90, 64), 13, torch.float16)
+    if layout == "NHD":
+        q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    if causal:                                  # causal q_len != kv_len is bottom-right aligned
+        pass
+    out, lse = sageattention.sageattn(q, k, v, tensor_layout=layout, is_causal=causal, return_lse=True)
+    th = (lambda t: t) if layout == "HND" else (lambda t: t.transpose(1, 2))
+    ref = orc.lse_reference(th(q).float().numpy(), th(k).float().numpy(), causal=causal)
+    assert lse.shape == (1, 4, 70) and lse.dtype == torch.float32
+    np.testing.assert_allclose(lse.numpy(), ref, atol=2e-3, rtol=1e-4)
+    assert out.shape == q.shape
+
+
+def test_invalid_layout_in_lse_raises_value_error():
+    q = _rand((1, 2, 8, 64), 14)
+    with pytest.raises(ValueError):
+        sageattention.core._lse(q, q, "BSHD", False, None)
+
+
+def test_variants_accept_and_ignore_kernel_kwargs():
+    q, k, v = (_rand((1, 2, 64, 64), s) for s in (15, 16, 17))
+    ref = sageattention.sageattn(q, k, v)
+    for n in VARIANTS:
+        out = getattr(sageattention, n)(q, k, v, tensor_layout="HND", smooth_k=True, pv_accum_dtype="fp32")
+        torch.testing.assert_close(out, ref, rtol=0, atol=0)
+    o, lse = sageattention.sageattn_qk_int8_pv_fp8_cuda(q, k, v, return_lse=True)
+    assert lse.shape == (1, 2, 64)
+
+
+def test_varlen_matches_per_sequence_attention():
+    H, D = 4, 64
+    lq, lk = [30, 0, 45, 12], [30, 20, 70, 5]
+    cq = torch.tensor([0] + np.cumsum(lq).tolist(), dtype=torch.int32)
+    ck = torch.tensor([0] + np.cumsum(lk).tolist(), dtype=torch.int32)
+    q = _rand((sum(lq), H, D), 18)
+    k, v = _rand((sum(lk), H, D), 19), _rand((sum(lk), H, D), 20)
+    for causal in (False, True):
+        out = sageattention.sageattn_varlen(q, k, v, cq, ck, max(lq), max(lk), is_causal=causal)
+        assert out.shape == q.shape
+        for i in range(len(lq)):
+            s, t = slice(int(cq[i]), int(cq[i + 1])), slice(int(ck[i]), int(ck[i + 1]))
+            if lq[i] == 0:
+                continue
+            qq, kk, vv = (x.transpose(0, 1)[None] for x in (q[s], k[t], v[t]))
+            if causal:
+                keep = torch.ones(lq[i], lk[i], dtype=torch.bool).tril(lk[i] - lq[i])
+                ref = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=keep)
+            else:
+                ref = F.scaled_dot_product_attention(qq, kk, vv)
+            torch.testing.assert_close(out[s], ref[0].transpose(0, 1))

@@ -1,0 +1,93 @@
+"""The C ABI library without a GPU: it loads, exports every symbol include/sage_capi.h declares, describes itself
+consistently with the committed manifest, and rejects invalid arguments with an error code and message before any
+HIP call (so these checks run on a machine without a GPU)."""
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+
+from cdna4_sage import _capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "sage_capi.h"
+
+pytestmark = pytest.mark.skipif(not _capi.LIB_PATH.exists(), reason="libsage_capi.so not built")
+
+P = 0x10000  # a 16-byte-aligned fake device address; never dereferenced because validation fails first
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(sage_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    lib = _capi.lib()
+    names = declared_symbols()
+    assert {"sage_quant_q", "sage_quant_kv", "sage_v_amax", "sage_attn_fwd", "sage_forward"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_capi.SIGNATURES), "ctypes signatures must cover exactly the header"
+
+
+def test_abi_version_kv_pad_and_manifest():
+    lib = _capi.lib()
+    assert lib.sage_abi_version() == _capi.ABI_VERSION
+    assert [_capi.kv_pad(s) for s in (1, 127, 128, 129, 4608, 67320)] == [128, 128, 128, 256, 4608, 67328]
+    built = json.loads(lib.sage_manifest_json().decode())
+    committed = json.loads((ROOT / "rdna4-sageattention_amd" / "cdna4_sage" / "manifest.json").read_text())
+    assert {k: v for k, v in committed.items() if k not in ("library", "build_flags")} == built
+    assert built["arch"] == "gfx950" and built["head_dims"] == [64, 128] and built["kv_block"] == 32
+
+
+def _err():
+    return _capi.lib().sage_last_error().decode()
+
+
+def test_quant_q_validation():
+    lib = _capi.lib()
+    ok = (P, 128 * 64, 128, 64, 1, 2, 64, 128, 0, 1.0, P, P, None)   # noqa: F841 (shape of a valid call)
+    assert lib.sage_quant_q(None, 0, 128, 0, 1, 1, 64, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
+    assert "q is NULL" in _err()
+    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 64, 96, 0, 1.0, P, P, None) == _capi.SAGE_ERR_UNSUPPORTED
+    assert "head_dim 96" in _err()
+    assert lib.sage_quant_q(P + 2, 0, 128, 0, 1, 1, 64, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
+    assert "aligned" in _err()
+    assert lib.sage_quant_q(P, 0, 100, 0, 1, 1, 64, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
+    assert "strides" in _err()
+    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 0, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 64, 128, 7, 1.0, P, P, None) == _capi.SAGE_ERR_UNSUPPORTED
+    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 64, 128, 0, 1.0, None, P, None) == _capi.SAGE_ERR_INVALID
+
+
+def test_kv_and_attention_validation():
+    lib = _capi.lib()
+    assert lib.sage_v_amax(P, 0, 128, 0, 1, 1, 64, 128, 0, None, None) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_quant_kv(P, 0, 128, 0, P, 0, 128, 0, 1, 1, 64, 128, 0, P, P, P, P + 8, None) == _capi.SAGE_ERR_INVALID
+    assert "16-byte" in _err()
+    args = dict(q8=P, qs=P, k8=P, ks=P, v8t=P, vs=P, out=P, osb=0, oss=128, osh=128, B=1, H=4, Hkv=2, Sq=64, Skv=64,
+                D=128, causal=0, out_dtype=0, lse=None, stream=None)
+
+    def attn(**kw):
+        a = dict(args, **kw)
+        return lib.sage_attn_fwd(*a.values())
+
+    assert attn(H=3) == _capi.SAGE_ERR_INVALID and "multiple" in _err()
+    assert attn(causal=1, Skv=65) == _capi.SAGE_ERR_UNSUPPORTED and "q_len == kv_len" in _err()
+    assert attn(D=256) == _capi.SAGE_ERR_UNSUPPORTED
+    assert attn(out_dtype=3) == _capi.SAGE_ERR_UNSUPPORTED
+    assert attn(q8=None) == _capi.SAGE_ERR_INVALID
+    assert attn(oss=100) == _capi.SAGE_ERR_INVALID
+    assert attn(Sq=0) == _capi.SAGE_ERR_INVALID
+
+
+def test_forward_validates_before_launching_and_python_raises():
+    lib = _capi.lib()
+    rc = lib.sage_forward(P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128, 1, 4, 2, 64, 80, 128, 0, 1, 1.0,
+                          P, P, P, P, P, P, None)
+    assert rc == _capi.SAGE_ERR_UNSUPPORTED and "causal" in _err()
+    with pytest.raises(_capi.SageError, match="head_dim 80"):
+        _capi.call("sage_quant_q", P, 0, 128, 0, 1, 1, 64, 80, 0, 1.0, P, P, None)
+    assert isinstance(ctypes.CDLL, type)

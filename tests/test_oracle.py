@@ -1,0 +1,263 @@
+"""Pins the CPU oracle (oracle/sage_oracle.py) with checks that do not restate its formulas: closed forms, exact
+rational arithmetic, torch's own E4M3 cast and inf-norm (the ops the reference calls), invariants of the quantizers
+and brute-force attention on cases whose answer is known."""
+import math
+import struct
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sage_oracle as orc
+
+F32 = np.float32
+
+
+def rn32(x: Fraction) -> np.float32:
+    """Correctly rounded float32 (round to nearest even) of an exact rational."""
+    if x == 0:
+        return F32(0.0)
+    s = -1 if x < 0 else 1
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 23)
+    qn = a / ulp
+    n = qn.numerator // qn.denominator
+    rem = qn - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return F32(s * float(n * ulp))
+
+
+# ------------------------------------------------------------------------------------------------ Hadamard
+@pytest.mark.parametrize("d", [1, 2, 4, 64, 128])
+def test_hadamard_closed_form(d):
+    h = orc.hadamard_pm1(d)
+    i = np.arange(d)
+    popc = np.vectorize(lambda x: bin(x).count("1"))(i[:, None] & i[None, :])
+    assert np.array_equal(h, (-1.0) ** popc)                      # H[i, j] = (-1)^popcount(i & j)
+    assert np.array_equal(h @ h.T, d * np.eye(d))                  # H H^T = d I
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fwht_matches_matrix_and_special_cases(d):
+    h = orc.hadamard_pm1(d)
+    eye = np.eye(d)
+    assert np.array_equal(orc.fwht_rows(eye), h)                    # e_i -> row i of H
+    c = np.full((3, d), 0.375)
+    exp = np.zeros((3, d))
+    exp[:, 0] = d * 0.375
+    assert np.array_equal(orc.fwht_rows(c), exp)                     # constant row -> d * c * e_0
+    x = np.random.default_rng(0).integers(-1000, 1000, (5, d)).astype(np.float64)
+    assert np.array_equal(orc.fwht_rows(x), x @ h)                  # exact on integers
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fwht_float32_is_correctly_rounded_exact_sum(dtype):
+    """The rotation used by the kernels is RN32 of the exact +-1 sum (checked with rational arithmetic)."""
+    d = 128
+    g = torch.Generator().manual_seed(1)
+    x = (torch.randn(6, d, generator=g) * torch.exp2(torch.randint(-8, 8, (6, d), generator=g).float())).to(dtype)
+    xs = x.float().numpy()
+    got = orc.fwht_rows(xs).astype(F32)
+    h = orc.hadamard_pm1(d).astype(int)
+    for r in range(xs.shape[0]):
+        fr = [Fraction(float(v)) for v in xs[r]]
+        for j in range(0, d, 7):
+            exact = sum((fr[i] if h[i, j] > 0 else -fr[i]) for i in range(d))
+            assert got[r, j] == rn32(exact), (r, j)
+
+
+# ------------------------------------------------------------------------------------------------ rounding helpers
+def test_round_half_away_matches_exact_definition():
+    """int8 conversion = trunc(RN32(y +- 0.5)) (reference: sage_quant.py:257): ties go away from zero and values
+    just below a half can still round up through the fp32 addition."""
+    ys = [0.5, -0.5, 1.5, -1.5, 2.5, 126.5, -126.5, 0.49999997, -0.49999997, 0.0, -0.0, 127.0, -127.0, 3.4999998]
+    ys += list(np.random.default_rng(2).uniform(-127.4, 127.4, 2000).astype(F32))
+    got = orc.round_half_away_i8(np.array(ys, dtype=F32))
+    for y, q in zip(ys, got):
+        y = F32(y)
+        t = rn32(Fraction(float(y)) + (Fraction(1, 2) if y >= 0 else Fraction(-1, 2)))
+        assert int(q) == int(math.trunc(float(t))), y
+    assert orc.round_half_away_i8(np.array([0.5 - 2**-25], dtype=F32))[0] == 1   # fp32(y + 0.5) == 1.0
+
+
+def _all_finite_e4m3():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    return codes, torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+
+
+def test_e4m3_decode_matches_torch():
+    codes, vals = _all_finite_e4m3()
+    assert np.array_equal(orc.e4m3_to_f32(codes), vals)
+
+
+def test_e4m3_encode_matches_torch_cast():
+    """fp32 -> E4M3FN (RNE with subnormals) against torch's own cast, exhaustively on every code, every midpoint
+    between neighbouring codes (ties to even) and their fp32 neighbours, plus random values in [-448, 448]."""
+    codes, vals = _all_finite_e4m3()
+    pos = np.unique(vals[vals >= 0])
+    mids = ((pos[1:].astype(np.float64) + pos[:-1]) / 2).astype(F32)
+    cand = np.concatenate([pos, mids, np.nextafter(mids, F32(0)), np.nextafter(mids, F32(1000))])
+    cand = np.concatenate([cand, -cand, np.random.default_rng(3).uniform(-448, 448, 200000).astype(F32),
+                           (np.random.default_rng(4).standard_normal(20000) * 2.0 ** -8).astype(F32)])
+    cand = np.clip(cand, F32(-448), F32(448)).astype(F32)
+    ref = torch.from_numpy(cand).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(orc.f32_to_e4m3(cand), ref)
+
+
+def test_division_sequence_of_the_kernels():
+    """The HIP quantizers divide by a shared scale s as y0 = x*r, e = fma(-y0, s, x), y = fma(e, r, y0) with
+    r = RN(1/s).  Exact rational arithmetic shows this equals IEEE RN(x / s), including adversarial scales whose
+    significand is all ones and quotients next to rounding ties."""
+    rng = np.random.default_rng(5)
+    cases = []
+    for _ in range(3000):
+        a = max(F32(abs(rng.standard_normal()) * 10 ** rng.uniform(-6, 3)), F32(1e-12))
+        s = F32(a / F32(127.0))
+        cases.append((F32(rng.uniform(-1, 1) * a), s))
+    for kk in range(500):
+        s = np.frombuffer(struct.pack("<I", 0x3F7FFFFF - kk), dtype=F32)[0] * F32(2.0 ** rng.integers(-20, 5))
+        x = F32(F32(rng.integers(-127, 128) + 0.5) * s)
+        cases += [(x, s), (np.nextafter(x, F32(np.inf)), s)]
+    fma = lambda a, b, c: rn32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))  # noqa: E731
+    for x, s in cases:
+        r = rn32(Fraction(1) / Fraction(float(s)))
+        y0 = F32(x * r)
+        y = fma(fma(-y0, s, x), r, y0)
+        assert y == F32(x / s), (x, s)
+
+
+# ------------------------------------------------------------------------------------------------ quantizers
+def _bf16(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16).float().numpy()
+
+
+def test_quant_q_invariants():
+    q = _bf16((2, 3, 97, 128), 6)
+    q[0, 0, 4] = 0.0
+    q8, qs = orc.quant_q(q)
+    x = orc.fwht_rows(q).astype(F32)
+    amax = np.abs(x).max(-1)
+    nz = amax > 1e-12
+    assert np.all(np.abs(q8.astype(int)).max(-1)[nz] == 127)         # full int8 range on every row
+    s = qs * 128                                                      # QS = s / RB, RB = head_dim
+    assert np.allclose(s[nz] * 127, amax[nz], rtol=1e-6)
+    assert np.all(np.abs(q8 * s[..., None] - x) <= s[..., None] * 0.5 * (1 + 1e-5))   # |dequant error| <= s/2
+    assert np.all(q8[0, 0, 4] == 0) and qs[0, 0, 4] == F32(F32(F32(1e-12) / F32(127)) / F32(128))
+
+
+def test_quant_kv_invariants_and_vector_norm():
+    k = _bf16((1, 2, 100, 64), 7)
+    v = _bf16((1, 2, 100, 64), 8, 3.0)
+    v[:, :, :, 5] = 0.0
+    k8, ks, v8, vs = orc.quant_kv(k, v, seq_pad=128)
+    # VS is torch.linalg.vector_norm(v, inf, dim=seq, dtype=float32), the reference's own op (_attention.py:121)
+    ref_vs = torch.linalg.vector_norm(torch.from_numpy(v).to(torch.bfloat16), ord=float("inf"), dim=2,
+                                      dtype=torch.float32).numpy()
+    assert np.array_equal(vs, ref_vs)
+    assert k8.shape == (1, 2, 128, 64) and ks.shape == (1, 2, 4)
+    assert np.all(k8[:, :, 100:] == 0) and np.all(v8[:, :, 100:] == 0)   # pad rows are zero
+    blk = np.abs(k8.astype(int)).reshape(1, 2, 4, 32, 64).max(axis=(-1, -2))
+    assert np.all(blk == 127)                                         # each 32-key block spans the int8 range
+    x = orc.fwht_rows(k).astype(F32)
+    # KS is max|x| / 127 of the block and is NOT divided by the rotation order (sage_quant.py:276-279)
+    assert np.allclose(ks[:, :, 0] * 127, np.abs(x[:, :, :32]).max(axis=(-1, -2)), rtol=1e-6)
+    dec = orc.e4m3_to_f32(v8[:, :, :100])
+    assert np.all(dec[..., 5] == 0)                                   # zero channel stays zero
+    am = np.abs(v).argmax(axis=2)
+    for c in (0, 7, 63):                                              # each channel's amax element maps to +-448
+        assert abs(dec[0, 0, am[0, 0, c], c]) == 448.0
+    rel = np.abs(dec * vs[:, :, None, :] / 448 - v) / np.maximum(np.abs(v), 1e-3)
+    assert np.all(rel[np.abs(v) > vs[:, :, None, :] / 16] <= 2.0 ** -4 + 1e-6)   # E4M3: 3 mantissa bits
+
+
+# ------------------------------------------------------------------------------------------------ attention
+def _cos(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return float((a * b).sum() / math.sqrt((a * a).sum() * (b * b).sum()))
+
+
+@pytest.mark.parametrize("block_n", [32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+def test_emulation_vs_float64_attention(block_n, causal):
+    """Config-1-like shape on CPU: the quantized path stays within the reference's accuracy (cos ~0.9992)."""
+    q, k, v = _bf16((1, 4, 512, 64), 9), _bf16((1, 4, 512, 64), 10), _bf16((1, 4, 512, 64), 11)
+    out = orc.sage_forward(q, k, v, causal=causal, block_n=block_n)
+    assert _cos(out, orc.sdpa_reference(q, k, v, causal=causal)) >= 0.999
+
+
+def test_emulation_single_key_returns_dequantized_v():
+    q, k, v = _bf16((1, 2, 5, 128), 12), _bf16((1, 2, 1, 128), 13), _bf16((1, 2, 1, 128), 14)
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    out = orc.attention(q8, qs, k8, ks, v8, vs, 1, out_dtype="f32")
+    deq = orc.e4m3_to_f32(v8[:, :, :1]) * vs[:, :, None, :] / 448.0
+    assert np.allclose(out, np.broadcast_to(deq, out.shape), rtol=1e-5, atol=1e-7)
+
+
+def test_emulation_causal_first_row_and_bottom_right():
+    q, k, v = _bf16((1, 1, 40, 64), 15), _bf16((1, 1, 40, 64), 16), _bf16((1, 1, 40, 64), 17)
+    out = orc.sage_forward(q, k, v, causal=True, block_n=32, out_dtype="f32")
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    deq0 = orc.e4m3_to_f32(v8[0, 0, 0]) * vs[0, 0] / 448.0
+    assert np.allclose(out[0, 0, 0], deq0, rtol=1e-5, atol=1e-7)     # row 0 sees key 0 only
+    # each row only depends on keys <= its index: changing the last key (in its own 32-key block, so no K scale
+    # of an earlier block moves) leaves every row of the first 32 unchanged
+    k2 = k.copy()
+    k2[..., -1, :] += 3.0
+    out2 = orc.sage_forward(q, k2, v, causal=True, block_n=32, out_dtype="f32")
+    assert np.array_equal(out[..., :32, :], out2[..., :32, :])
+    assert not np.array_equal(out[..., 39, :], out2[..., 39, :])
+
+
+def test_emulation_softmax_bookkeeping_gives_exact_lse():
+    """The running max / lazy rescale / running sum must reproduce the logsumexp of the quantized logits
+    S * QS * KS * sm computed directly; this fails for a dropped correction term or a misplaced K scale."""
+    q, k, v = _bf16((1, 2, 64, 128), 18), _bf16((1, 2, 300, 128), 19, 2.0), _bf16((1, 2, 300, 128), 20)
+    k[:, :, 100:140] *= 8.0                      # blocks with very different K scales
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    for bn in (32, 64):
+        _, m, l = orc.attention(q8, qs, k8, ks, v8, vs, 300, block_n=bn, return_stats=True)
+        cl = orc.logit_scale_base(128) * qs
+        lse2 = cl.astype(np.float64) * m + np.log2(l.astype(np.float64))
+        ksr = np.repeat(ks, 32, axis=-1)[:, :, :300]
+        s = np.einsum("bhqd,bhkd->bhqk", q8.astype(np.float64), k8[:, :, :300].astype(np.float64))
+        logit2 = s * cl[..., None].astype(np.float64) * ksr[:, :, None, :]
+        mx = logit2.max(-1)
+        exact = mx + np.log2(np.exp2(logit2 - mx[..., None]).sum(-1))
+        assert np.allclose(lse2, exact, rtol=0, atol=2e-5), bn
+
+
+def test_emulation_gqa_equals_repeated_heads():
+    q, k, v = _bf16((1, 4, 70, 64), 21), _bf16((1, 1, 90, 64), 22), _bf16((1, 1, 90, 64), 23)
+    a = orc.sage_forward(q, k, v, block_n=64)
+    b = orc.sage_forward(q, np.repeat(k, 4, 1), np.repeat(v, 4, 1), block_n=64)
+    assert np.array_equal(a, b)
+
+
+def test_v8_device_layout_permutation():
+    v8 = np.random.default_rng(24).integers(0, 256, (1, 2, 128, 64)).astype(np.uint8)
+    t = orc.v8_to_device_layout(v8)
+    for key in range(128):
+        grp, g, h, r = key // 64, (key % 64) // 8, (key // 4) % 2, key % 4
+        assert np.array_equal(t[:, :, :, 64 * grp + 32 * h + 4 * g + r], v8[:, :, key, :])
+    assert np.array_equal(orc.v8_from_device_layout(t), v8)
+
+
+def test_lse_reference_matches_torch_logsumexp():
+    q, k = _bf16((1, 2, 50, 64), 25), _bf16((1, 2, 80, 64), 26)
+    for causal in (False, True):
+        got = orc.lse_reference(q, k, causal=causal)
+        sc = torch.from_numpy(q).double() @ torch.from_numpy(k).double().transpose(-1, -2) * 64 ** -0.5
+        if causal:
+            sc.masked_fill_(torch.ones(50, 80, dtype=torch.bool).tril(80 - 50).logical_not(), float("-inf"))
+        assert np.allclose(got, torch.logsumexp(sc, -1).numpy(), atol=1e-10)
