@@ -38,21 +38,29 @@ template <int ROW_BYTES> __device__ __forceinline__ int swz(int row, int chunk) 
   return chunk ^ ((row >> 2) & 3);
 }
 
+// Direct global -> LDS copy of 16 bytes per lane: the data lands at LDS address (M0 base) + 16 * lane, so a wave
+// writes one contiguous KiB; `lds` must be wave-uniform.
+__device__ __forceinline__ void copy16_to_lds(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
 template <int D, bool CAUSAL, int OUT_DT>
-__global__ __launch_bounds__(ATT_THREADS, 2) void attn_kernel(
+__global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ qs, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
     int Sq, int Skv, int Skp, int q_tiles, int total, float c0) {
   constexpr int BN = ATT_BN;
-  constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D])
+  constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
   constexpr int VTILE = D * BN;      // bytes of the V tile  ([D channels][64 keys])
+  constexpr int TILE = KTILE + VTILE;
   constexpr int NQK = D / 32;        // i8 MFMAs (K = 32 dims) per 32-key block
   constexpr int NPV = D / 32;        // fp8 MFMAs (M = 32 channels) per tile
   constexpr int KCH = D / 16;        // 16-byte chunks per K row
-  constexpr int NKL = KTILE / 16 / ATT_THREADS;  // K chunks per thread per tile
-  constexpr int NVL = VTILE / 16 / ATT_THREADS;  // V chunks per thread per tile
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][KTILE + VTILE];
+  constexpr int KLOADS = KTILE / 1024 / 4;  // 1 KiB direct loads per wave per tile (4 waves)
+  constexpr int VLOADS = VTILE / 1024 / 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][TILE];
 
   // ---- work decode ----
   const int logical = xcd_remap(blockIdx.x, total);
@@ -85,42 +93,44 @@ __global__ __launch_bounds__(ATT_THREADS, 2) void attn_kernel(
   int kv_end = Skv;
   if (CAUSAL) kv_end = min(Skv, qt * ATT_BM + ATT_BM + off);
   const int ntiles = (kv_end + BN - 1) / BN;
-  const int wave_last_key = CAUSAL ? min(Skv - 1, q0 + 31 + off) : Skv - 1;
 
   const int8_t* kbase = k8 + (int64_t)bhk * Skp * D;
   const uint8_t* vbase = v8t + (int64_t)bhk * D * Skp;
   const float* ksb = ks + (int64_t)bhk * (Skp / SAGE_KV_BLOCK);
 
-  uint4 kreg[NKL], vreg[NVL];
-  auto load_tile = [&](int t) {
+  // Source of each lane's direct loads.  Load j of wave w fills LDS chunk L = (w * LOADS + j) * 64 + lane of the
+  // region, which must receive the tile chunk that the swizzled layout stores there.
+  int koff[KLOADS];
+  int64_t voff[VLOADS];
 #pragma unroll
-    for (int i = 0; i < NKL; ++i) {
-      const int c = tid + i * ATT_THREADS;
-      kreg[i] = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * KTILE + c * 16);
-    }
+  for (int j = 0; j < KLOADS; ++j) {
+    const int L = (wave * KLOADS + j) * 64 + lane;
+    const int row = L / KCH;
+    koff[j] = row * D + swz<D>(row, L % KCH) * 16;  // swz is an involution: stored chunk c' holds chunk c' ^ s
+  }
 #pragma unroll
-    for (int i = 0; i < NVL; ++i) {
-      const int c = tid + i * ATT_THREADS;
-      const int d = c >> 2, col = c & 3;
-      vreg[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)d * Skp + t * BN + col * 16);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint8_t* kt = smem[buf];
-    uint8_t* vt = smem[buf] + KTILE;
+  for (int j = 0; j < VLOADS; ++j) {
+    const int L = (wave * VLOADS + j) * 64 + lane;
+    const int d = L >> 2;
+    voff[j] = (int64_t)d * Skp + swz<BN>(d, L & 3) * 16;
+  }
+#define SAGE_ISSUE_TILE(T, BUF)                                                                            \
+  do {                                                                                                     \
+    const int tt_ = (T);                                                                                   \
+    uint8_t* dst_ = smem[BUF];                                                                             \
+    _Pragma("unroll") for (int j_ = 0; j_ < KLOADS; ++j_)                                                  \
+      copy16_to_lds(kbase + (int64_t)tt_ * KTILE + koff[j_], dst_ + (wave * KLOADS + j_) * 1024);          \
+    _Pragma("unroll") for (int j_ = 0; j_ < VLOADS; ++j_)                                                  \
+      copy16_to_lds(vbase + voff[j_] + tt_ * BN, dst_ + KTILE + (wave * VLOADS + j_) * 1024);              \
+  } while (0)
+
+  // Lane-constant LDS offsets of the MFMA operands.  For rows 32 kb + ln the K swizzle does not depend on kb, and
+  // for channel rows 32 j + ln the V swizzle does not depend on j, so one offset per step serves every block.
+  int ko[NQK];
 #pragma unroll
-    for (int i = 0; i < NKL; ++i) {
-      const int c = tid + i * ATT_THREADS;
-      const int row = c / KCH, col = c % KCH;
-      *reinterpret_cast<uint4*>(kt + row * D + swz<D>(row, col) * 16) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < NVL; ++i) {
-      const int c = tid + i * ATT_THREADS;
-      const int d = c >> 2, col = c & 3;
-      *reinterpret_cast<uint4*>(vt + d * BN + swz<BN>(d, col) * 16) = vreg[i];
-    }
-  };
+  for (int i = 0; i < NQK; ++i) ko[i] = ln * D + swz<D>(ln, 2 * i + hf) * 16;
+  const int vo0 = ln * BN + swz<BN>(ln, 2 * hf) * 16;
+  const int vo1 = ln * BN + swz<BN>(ln, 2 * hf + 1) * 16;
 
   v16f o[NPV];
 #pragma unroll
@@ -128,107 +138,100 @@ __global__ __launch_bounds__(ATT_THREADS, 2) void attn_kernel(
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
   float m = -INFINITY, l = 0.0f;
+  v8i pb = {};  // E4M3 probabilities (B operand of the PV MFMA); each cvt rewrites one half, so no clearing
 
-  load_tile(0);
-  store_tile(0);
+  // One tile: S^T = K Q^T (int8 MFMA), online softmax with the reference's lazy rescale, O^T += V^T P^T (fp8 MFMA).
+#define SAGE_TILE(T, MASKED)                                                                               \
+  do {                                                                                                     \
+    const int t_ = (T);                                                                                    \
+    const uint8_t* kt_ = smem[t_ & 1];                                                                     \
+    const uint8_t* vt_ = smem[t_ & 1] + KTILE;                                                             \
+    v16i s_[2];                                                                                            \
+    _Pragma("unroll") for (int i_ = 0; i_ < NQK; ++i_) {                                                   \
+      const v4i k0_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_]);                                         \
+      const v4i k1_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_] + 32 * D);                                \
+      s_[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0_, qa[i_], i_ == 0 ? zero16 : s_[0], 0, 0, 0);       \
+      s_[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], i_ == 0 ? zero16 : s_[1], 0, 0, 0);       \
+    }                                                                                                      \
+    float sf_[2][16];                                                                                      \
+    _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] = (float)s_[kb_][v_];                 \
+    if (MASKED) {                                                                                          \
+      const int kstart_ = t_ * BN;                                                                         \
+      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
+          const int key_ = kstart_ + 32 * kb_ + 8 * (v_ >> 2) + 4 * hf + (v_ & 3);                         \
+          if (key_ >= Skv || (CAUSAL && key_ > qr + off)) sf_[kb_][v_] = -INFINITY;                        \
+        }                                                                                                  \
+    }                                                                                                      \
+    float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                              \
+    _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                    \
+      mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                      \
+      mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                      \
+    }                                                                                                      \
+    mx0_ = fmaxf(mx0_, xor32_f32(mx0_));                                                                   \
+    mx1_ = fmaxf(mx1_, xor32_f32(mx1_));                                                                   \
+    const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
+    const float rowmax_ = fmaxf(mx0_ * ks0_, mx1_ * ks1_);                                                 \
+    const float mcand_ = fmaxf(m, rowmax_);                                                                \
+    const bool need_ = (mcand_ - m) * cl > 8.0f;                                                           \
+    const float mnew_ = need_ ? mcand_ : m;                                                                \
+    const float corr_ = __builtin_amdgcn_exp2f((m - mnew_) * cl);                                          \
+    const float neg_ = 0.0f - cl * mnew_;                                                                  \
+    const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
+    float psum_ = 0.0f;                                                                                    \
+    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
+      sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, neg_));                         \
+      psum_ += sf_[0][v_];                                                                                 \
+    }                                                                                                      \
+    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
+      sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, neg_));                         \
+      psum_ += sf_[1][v_];                                                                                 \
+    }                                                                                                      \
+    l = corr_ * l + psum_;                                                                                 \
+    m = mnew_;                                                                                             \
+    if (__ballot(need_) != 0) {                                                                            \
+      _Pragma("unroll") for (int i_ = 0; i_ < NPV; ++i_)                                                   \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) o[i_][v_] *= corr_;                              \
+    }                                                                                                      \
+    _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                     \
+      const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                         \
+      pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
+      pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);        \
+    }                                                                                                      \
+    _Pragma("unroll") for (int j_ = 0; j_ < NPV; ++j_) {                                                   \
+      const v4i a0_ = *reinterpret_cast<const v4i*>(vt_ + vo0 + j_ * 32 * BN);                             \
+      const v4i a1_ = *reinterpret_cast<const v4i*>(vt_ + vo1 + j_ * 32 * BN);                             \
+      const v8i va_ = {a0_[0], a0_[1], a0_[2], a0_[3], a1_[0], a1_[1], a1_[2], a1_[3]};                    \
+      o[j_] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va_, pb, o[j_], 0, 0, 0, 0, 0, 0);           \
+    }                                                                                                      \
+  } while (0)
+
+  // Tiles before `t_mask` need no key mask for any row of this wave: they end below Skv and (causal) below the
+  // wave's first row's diagonal.  The remaining tiles (at most three) run the masked variant.  The direct loads
+  // are asynchronous writes to LDS the compiler does not track, hence the explicit vmcnt waits before barriers.
+  int t_mask = Skv / BN;
+  if (CAUSAL) t_mask = min(t_mask, max(0, (q0 + off + 1) / BN));
+  t_mask = min(t_mask, ntiles);
+  const v16i zero16 = {};
+  SAGE_ISSUE_TILE(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1);
-    const int kstart = t * BN;
-    if (kstart <= wave_last_key) {
-      const uint8_t* kt = smem[buf];
-      const uint8_t* vt = smem[buf] + KTILE;
-      // ---- S^T = K Q^T ----
-      v16i s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) s[kb][v] = 0;
-        const int row = 32 * kb + ln;
-#pragma unroll
-        for (int i = 0; i < NQK; ++i) {
-          const v4i ka = *reinterpret_cast<const v4i*>(kt + row * D + swz<D>(row, 2 * i + hf) * 16);
-          s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka, qa[i], s[kb], 0, 0, 0);
-        }
-      }
-      // ---- online softmax ----
-      float sf[2][16];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sf[kb][v] = (float)s[kb][v];
-      const bool need_mask = (kstart + BN > Skv) || (CAUSAL && kstart + BN - 1 > q0 + off);
-      if (need_mask) {
-        const int last = qr + off;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int key = kstart + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
-            if (key >= Skv || (CAUSAL && key > last)) sf[kb][v] = -INFINITY;
-          }
-      }
-      float mx0 = sf[0][0], mx1 = sf[1][0];
-#pragma unroll
-      for (int v = 1; v < 16; ++v) {
-        mx0 = fmaxf(mx0, sf[0][v]);
-        mx1 = fmaxf(mx1, sf[1][v]);
-      }
-      mx0 = fmaxf(mx0, xor32_f32(mx0));
-      mx1 = fmaxf(mx1, xor32_f32(mx1));
-      const float ks0 = ksb[2 * t], ks1 = ksb[2 * t + 1];
-      const float rowmax = fmaxf(mx0 * ks0, mx1 * ks1);
-      const float m_cand = fmaxf(m, rowmax);
-      const bool need = (m_cand - m) * cl > 8.0f;
-      const float m_new = need ? m_cand : m;
-      const float corr = __builtin_amdgcn_exp2f((m - m_new) * cl);
-      const float neg = 0.0f - cl * m_new;
-      const float ct0 = cl * ks0, ct1 = cl * ks1;
-      float p[2][16];
-      float psum = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        p[0][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf[0][v], ct0, neg));
-        psum += p[0][v];
-      }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        p[1][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf[1][v], ct1, neg));
-        psum += p[1][v];
-      }
-      l = corr * l + psum;
-      m = m_new;
-      if (__builtin_amdgcn_read_exec() & __ballot(need)) {
-#pragma unroll
-        for (int i = 0; i < NPV; ++i)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) o[i][v] *= corr;
-      }
-      // ---- P -> E4M3, B operand byte t = 16 kb + v ----
-      v8i pb;
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        const int kb = w >> 2, v0 = 4 * (w & 3);
-        int d = 0;
-        d = __builtin_amdgcn_cvt_pk_fp8_f32(p[kb][v0], p[kb][v0 + 1], d, false);
-        d = __builtin_amdgcn_cvt_pk_fp8_f32(p[kb][v0 + 2], p[kb][v0 + 3], d, true);
-        pb[w] = d;
-      }
-      // ---- O^T += V^T P^T ----
-#pragma unroll
-      for (int i = 0; i < NPV; ++i) {
-        const int d = 32 * i + ln;
-        const v4i a0 = *reinterpret_cast<const v4i*>(vt + d * BN + swz<BN>(d, 2 * hf) * 16);
-        const v4i a1 = *reinterpret_cast<const v4i*>(vt + d * BN + swz<BN>(d, 2 * hf + 1) * 16);
-        const v8i va = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        o[i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, pb, o[i], 0, 0, 0, 0, 0, 0);
-      }
-    }
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
+  int t = 0;
+  for (; t < t_mask; ++t) {
+    if (t + 1 < ntiles) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+    SAGE_TILE(t, false);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
+  for (; t < ntiles; ++t) {
+    if (t + 1 < ntiles) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+    SAGE_TILE(t, true);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+#undef SAGE_ISSUE_TILE
+#undef SAGE_TILE
 
   // ---- epilogue ----
   const float lt = l + xor32_f32(l);
@@ -241,11 +244,11 @@ __global__ __launch_bounds__(ATT_THREADS, 2) void attn_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c = 32 * i + 8 * g + 4 * hf;
-        const v4f sc = *reinterpret_cast<const v4f*>(vsr + c);
-        const uint32_t e0 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 0] * inv) * sc[0]);
-        const uint32_t e1 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 1] * inv) * sc[1]);
-        const uint32_t e2 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 2] * inv) * sc[2]);
-        const uint32_t e3 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 3] * inv) * sc[3]);
+        const v4f sc4 = *reinterpret_cast<const v4f*>(vsr + c);
+        const uint32_t e0 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 0] * inv) * sc4[0]);
+        const uint32_t e1 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 1] * inv) * sc4[1]);
+        const uint32_t e2 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 2] * inv) * sc4[2]);
+        const uint32_t e3 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 3] * inv) * sc4[3]);
         *reinterpret_cast<uint2*>(orow + c) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
       }
     }
