@@ -98,6 +98,17 @@ def cpu_baseline(cfg, target_s=15.0):
     }
 
 
+def profiled_traffic(cfg_key):
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (config 2)."""
+    f = ROOT / "profiles" / "flux_config2_hbm_traffic.md"
+    if cfg_key != "2" or not f.exists():
+        return None, None
+    for line in f.read_text().splitlines():
+        if line.startswith("attn_kernel traffic_bytes_per_launch:"):
+            return int(line.split(":")[1]), str(f.relative_to(ROOT))
+    return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,6 +117,8 @@ def main():
     ap.add_argument("--config", default="2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run one plain device copy of this many MiB first (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported (each call is a single-device "
@@ -123,6 +136,12 @@ def main():
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_probe_mib > 0:
+        src = torch.ones(args.copy_probe_mib * 2**20 // 4, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log(f"device {torch.cuda.get_device_name(dev)} arch {_attention.device_arch(dev)}; workload {cfg.name}")
     q, k, v = (t.to(dev) for t in make_inputs(cfg))
     torch.cuda.synchronize()
@@ -196,6 +215,7 @@ def main():
     torch.cuda.synchronize()
     ms_sdpa = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    traffic, traffic_src = profiled_traffic(args.config)
     result = {
         "metric": "attention TOPS + ms/call (Flux 24x4608x128), % of int8/fp8 MFMA peak",
         "value": round(tops, 2),
@@ -212,7 +232,8 @@ def main():
         "config": {"workload": cfg.name, "B": B, "H": H, "Hkv": Hkv, "Sq": S, "Skv": S, "D": D,
                    "layout": "HND", "input_dtype": str(q.dtype).replace("torch.", ""), "causal": cfg.causal},
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(attn_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "attn_kernel<128,false,bf16>", "ms_per_launch": round(t_attn, 5),
                      "ops_per_launch": ops},
         "detail": {
