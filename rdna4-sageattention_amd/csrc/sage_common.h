@@ -53,13 +53,14 @@ template <int DT> __device__ __forceinline__ uint32_t f32_to_out_bits(float f) {
 constexpr int DPP_QUAD_XOR1 = 0xB1;  // [1, 0, 3, 2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;  // [2, 3, 0, 1]
 
+// (quad_perm reads a valid lane for every lane, so the DPP "old" value is never used: mov_dpp needs no copy of it)
 template <int CTRL> __device__ __forceinline__ float dpp_f32(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
 }
 template <int CTRL> __device__ __forceinline__ double dpp_f64(double x) {
   const int lo = __double2loint(x), hi = __double2hiint(x);
-  const int plo = __builtin_amdgcn_update_dpp(0, lo, CTRL, 0xF, 0xF, false);
-  const int phi = __builtin_amdgcn_update_dpp(0, hi, CTRL, 0xF, 0xF, false);
+  const int plo = __builtin_amdgcn_mov_dpp(lo, CTRL, 0xF, 0xF, false);
+  const int phi = __builtin_amdgcn_mov_dpp(hi, CTRL, 0xF, 0xF, false);
   return __hiloint2double(phi, plo);
 }
 // value held by lane (lane ^ 32)
@@ -113,8 +114,10 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
   return __builtin_fmaf(e, r, y0);
 }
 
+// trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)); copysign gives -0.5 only for y < 0 or y = -0, and -0 - 0.5 truncates
+// to 0 like +0 + 0.5 does, so one bitfield insert replaces the compare and select
 __device__ __forceinline__ int round_half_away(float y) {
-  const float t = y >= 0.0f ? y + 0.5f : y - 0.5f;
+  const float t = y + __builtin_copysignf(0.5f, y);
   return (int)t;  // v_cvt_i32_f32 truncates toward zero
 }
 
