@@ -188,18 +188,23 @@ def main():
         L.sage_quant_kv(k.data_ptr(), *ks_, v.data_ptr(), *vs_, B, Hkv, S, D, dt, vs.data_ptr(), k8.data_ptr(),
                         ks.data_ptr(), v8t.data_ptr(), st)
 
-    def k_attn():
+    n_full, chunks, ws_bytes = _capi.attn_plan(0, B, H, S, S, D, cfg.causal)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    def k_attn(split=True):
         L.sage_attn_fwd(q8.data_ptr(), qs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(), vs.data_ptr(),
                         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), B, H, Hkv, S, S, D,
-                        int(cfg.causal), dt, None, st)
+                        int(cfg.causal), dt, None, ws.data_ptr() if split and ws_bytes else None,
+                        ws_bytes if split else 0, st)
 
-    k_amax(); k_q(); k_kv(); k_attn()
+    k_amax(); k_q(); k_kv(); k_attn(); k_attn(False)
     torch.cuda.synchronize()
     it = args.kernel_iters
     t_amax = time_events(k_amax, it)
     t_q = time_events(k_q, it)
     t_kv = time_events(k_kv, it)
     t_attn = time_events(k_attn, it)
+    t_attn_whole = time_events(lambda: k_attn(False), it)
     attn_tflops = ops / (t_attn * 1e-3) / 1e12
     q_bytes = cfg.quant_q_bytes()
     kv_bytes = cfg.quant_kv_bytes(skp)
@@ -234,12 +239,15 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "attn_kernel<128,false,bf16>", "ms_per_launch": round(t_attn, 5),
-                     "ops_per_launch": ops},
+                     "kernel": f"attn_kernel<{D},{str(cfg.causal).lower()},bf16>"
+                               + (" + attn_merge_kernel" if chunks > 1 else ""),
+                     "ms_per_launch": round(t_attn, 5), "ops_per_launch": ops,
+                     "plan": {"whole_tiles": n_full, "split_tiles": B * H * ((S + 127) // 128) - n_full,
+                              "kv_chunks": chunks, "workspace_bytes": ws_bytes}},
         "detail": {
             "call_frac_of_peak": round(tops / MFMA_PEAK_TFLOPS, 4),
             "kernel_ms": {"v_amax+fill": round(t_amax, 5), "quant_q": round(t_q, 5), "quant_kv": round(t_kv, 5),
-                          "attn": round(t_attn, 5)},
+                          "attn": round(t_attn, 5), "attn_without_split": round(t_attn_whole, 5)},
             "quant_q_GBps": round(q_bytes / (t_q * 1e-3) / 1e9, 1),
             "quant_kv_GBps": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
             "hbm_peak_GBps": HBM_PEAK_GBS,

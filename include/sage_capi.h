@@ -25,6 +25,11 @@
  *                                         stored at position 32h + 4g + r (the order the attention kernel's fp8 MFMA
  *                                         operand wants); keys >= Skv are zero
  *  - VS  fp32  [B, Hkv, D]                per-channel max |v| over the sequence
+ *
+ * Workspace: sage_attn_fwd / sage_forward may split the key range of the query tiles of a short last round over
+ * several workgroups (a plan that depends on the problem shape and the device's CU count, see sage_attn_plan); the
+ * partial softmax state of those tiles lives in a caller-provided workspace, 256-byte aligned.  Passing NULL runs
+ * every tile whole (same results up to float rounding of the merge, lower throughput when the last round is short).
  */
 #ifndef SAGE_CAPI_H
 #define SAGE_CAPI_H
@@ -86,15 +91,29 @@ int sage_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const vo
                   uint8_t* v8t, void* stream);
 
 /*
+ * Work plan of sage_attn_fwd on the current device: query tiles (128 rows of one batch and head, numbered
+ * ((b * H + h) * ceil(Sq / 128) + tile)) below *n_full run whole; each later tile splits its key tiles of 64 keys into
+ * *chunks contiguous ranges merged by a second kernel.  *workspace_bytes is the workspace the split needs (0 when
+ * nothing is split).  Output pointers may be NULL.  No counterpart in the reference (its launch is one workgroup per
+ * query tile, src/rdna4_sage/_attention.py:133-139).
+ */
+int sage_attn_plan(int B, int H, int Sq, int Skv, int D, int causal, int* n_full, int* chunks, int64_t* workspace_bytes);
+
+/*
  * int8 QK^T / fp8 PV flash attention with the reference's online softmax (lazy rescale, threshold 8 in log2
  * units), causal (bottom-right aligned, requires Sq == Skv) and grouped-query heads (H % Hkv == 0).
  * Replaces the attn launch of src/rdna4_sage/_attention.py:133-139 (kernarg "<4Q3i4x6Q2i", build_kernels.py:331).
  * out: out + b*osb + s*oss + h*osh (element strides, head_dim contiguous), dtype out_dtype.
  * lse: optional fp32 [B, H, Sq] (natural-log logsumexp of the quantized logits); pass NULL to skip.
+ * workspace: NULL, or at least the sage_attn_plan bytes for this shape (see "Workspace" above).
  */
 int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
                   const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq,
-                  int Skv, int D, int causal, int out_dtype, float* lse, void* stream);
+                  int Skv, int D, int causal, int out_dtype, float* lse, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
+/* Workspace bytes sage_forward needs for this shape on the current device. */
+int sage_forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* workspace_bytes);
 
 /*
  * The whole path in one call: v_amax, quant_q, quant_kv, attention, on one stream.  Replaces the body of
@@ -104,7 +123,8 @@ int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const flo
 int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                  int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb, int64_t oss,
                  int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float qs_mul,
-                 int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* stream);
+                 int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -215,18 +215,56 @@ def logit_scale_base(d: int) -> np.float32:
 
 
 def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n: int = 32,
-              out_dtype: str = "bf16", threshold: float = RESCALE_THRESHOLD, return_stats: bool = False):
+              out_dtype: str = "bf16", threshold: float = RESCALE_THRESHOLD, return_stats: bool = False,
+              kv_split=None):
     """Quantized attention as the reference kernel computes it.
 
     q8 [B, H, Sq, D] int8, qs [B, H, Sq] f32, k8 [B, Hkv, Sp, D] int8, ks [B, Hkv, Sp/32] f32,
     v8 [B, Hkv, Sp, D] E4M3 bits (natural key order), vs [B, Hkv, D] f32.  Returns float32 [B, H, Sq, D]
-    holding values rounded to ``out_dtype`` ("bf16", "f16" or "f32" for no rounding)."""
+    holding values rounded to ``out_dtype`` ("bf16", "f16" or "f32" for no rounding).
+
+    ``kv_split = (chunks, rows)``, rows a bool array [B, H, Sq], emulates the gfx950 kernel's split tiles (no
+    counterpart in the reference): for those rows the key tiles run as ``chunks`` contiguous ranges (range c =
+    tiles [c * n // chunks, (c + 1) * n // chunks)), each with its own online softmax from m = -inf, merged with
+    M = max m_c, w_c = exp2((m_c - M) * cl), L = sum w_c l_c, O = sum w_c O_c (float32, chunk order), then the
+    usual epilogue with L."""
     B, H, Sq, D = q8.shape
-    Hkv, Sp = k8.shape[1], k8.shape[2]
+    Hkv = k8.shape[1]
     assert block_n % KV_BLOCK == 0 and H % Hkv == 0
     grp = H // Hkv
-    c0 = logit_scale_base(D)
-    cl = (c0 * qs.astype(F32)).astype(F32)                      # [B, H, Sq]
+    hk = np.arange(H) // grp
+    cl = (logit_scale_base(D) * qs.astype(F32)).astype(F32)      # [B, H, Sq]
+    n_tiles = (seq_kv + block_n - 1) // block_n
+    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles)
+    if kv_split is not None:
+        chunks, rows = kv_split
+        parts = [_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold,
+                                 c * n_tiles // chunks, (c + 1) * n_tiles // chunks) for c in range(chunks)]
+        mm = parts[0][1]
+        for _, mc, _ in parts[1:]:
+            mm = np.maximum(mm, mc)
+        ll = np.zeros_like(l)
+        oo = np.zeros_like(o)
+        for oc, mc, lc in parts:
+            w = np.exp2(((mc - mm).astype(F32) * cl).astype(F32)).astype(F32)
+            ll = (ll + (w * lc).astype(F32)).astype(F32)
+            oo = (oo + (w[..., None] * oc).astype(F32)).astype(F32)
+        o = np.where(rows[..., None], oo, o)
+        m = np.where(rows, mm, m)
+        l = np.where(rows, ll, l)
+    inv = (F32(1.0 / 448.0) / l).astype(F32)
+    out = ((o * inv[..., None]).astype(F32) * vs[:, hk][:, :, None, :].astype(F32)).astype(F32)
+    out = round_output(out, out_dtype)
+    if return_stats:
+        return out, m, l
+    return out
+
+
+def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi):
+    """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row."""
+    B, H, Sq, D = q8.shape
+    Hkv, Sp = k8.shape[1], k8.shape[2]
+    hk = np.arange(H) // (H // Hkv)
     q8f = q8.astype(F32)
     k8f = k8.astype(F32)
     v8f = e4m3_to_f32(v8)
@@ -236,9 +274,7 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     rows = np.arange(Sq)
     causal_off = seq_kv - Sq
     nsub = block_n // KV_BLOCK
-    n_tiles = (seq_kv + block_n - 1) // block_n
-    hk = np.arange(H) // grp
-    for t in range(n_tiles):
+    for t in range(t_lo, t_hi):
         j0 = t * block_n
         j1 = min(j0 + block_n, Sp)
         cols = np.arange(j0, j0 + block_n)
@@ -274,12 +310,18 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
         p8 = e4m3_to_f32(f32_to_e4m3(p))
         o = (o + np.matmul(p8, vt[:, hk])).astype(F32)
         m = m_new
-    inv = (F32(1.0 / 448.0) / l).astype(F32)
-    out = ((o * inv[..., None]).astype(F32) * vs[:, hk][:, :, None, :].astype(F32)).astype(F32)
-    out = round_output(out, out_dtype)
-    if return_stats:
-        return out, m, l
-    return out
+    return o, m, l
+
+
+def split_rows(B: int, H_total: int, Sq: int, n_full: int, heads=None, block_m: int = 128) -> np.ndarray:
+    """Bool [B, len(heads), Sq]: rows of the query tiles numbered >= n_full, where the gfx950 kernel numbers the
+    tile of row r of batch b, head h as (b * H_total + h) * ceil(Sq / block_m) + r // block_m.  ``heads`` lists the
+    heads of a sample by their index in the full problem (default: all H_total heads)."""
+    heads = np.arange(H_total) if heads is None else np.asarray(heads)
+    q_tiles = (Sq + block_m - 1) // block_m
+    tile = ((np.arange(B)[:, None, None] * H_total + heads[None, :, None]) * q_tiles
+            + (np.arange(Sq) // block_m)[None, None, :])
+    return tile >= n_full
 
 
 def round_output(x: np.ndarray, out_dtype: str) -> np.ndarray:

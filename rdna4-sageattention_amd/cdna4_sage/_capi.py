@@ -9,6 +9,7 @@ context and streams, which is the reason the reference looks the runtime up in /
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from pathlib import Path
 
@@ -18,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsage_capi.so"
 
 SAGE_OK, SAGE_ERR_INVALID, SAGE_ERR_UNSUPPORTED, SAGE_ERR_HIP = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F16 = 0, 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()
@@ -36,9 +37,11 @@ SIGNATURES = {
     "sage_quant_q": ([_P, _L, _L, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P], _I),
     "sage_v_amax": ([_P, _L, _L, _L, _I, _I, _I, _I, _I, _P, _P], _I),
     "sage_quant_kv": ([_P, _L, _L, _L, _P, _L, _L, _L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
-    "sage_attn_fwd": ([_P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "sage_attn_plan": ([_I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
+    "sage_attn_fwd": ([_P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _L, _P], _I),
+    "sage_forward_workspace": ([_I, _I, _I, _I, _I, _I, _I, _P], _I),
     "sage_forward": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
-                      _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P], _I),
+                      _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
 }
 
 
@@ -78,3 +81,13 @@ def call(name: str, *args) -> None:
 
 def kv_pad(skv: int) -> int:
     return int(lib().sage_kv_pad(int(skv)))
+
+
+@functools.lru_cache(maxsize=4096)
+def attn_plan(device_index: int, B: int, H: int, Sq: int, Skv: int, D: int, causal: bool):
+    """(n_full, chunks, workspace_bytes) of sage_attn_fwd for this shape on device `device_index`."""
+    n_full, chunks, ws = ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    with torch.cuda.device(device_index):
+        call("sage_attn_plan", B, H, Sq, Skv, D, int(causal), ctypes.byref(n_full), ctypes.byref(chunks),
+             ctypes.byref(ws))
+    return n_full.value, chunks.value, ws.value

@@ -45,12 +45,19 @@ __device__ __forceinline__ void copy16_to_lds(const void* g, void* lds) {
                                    (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
+constexpr int ATT_MAX_CHUNKS = 16;
+
+// Workspace of a split launch (units = split tiles x chunks): O partials fp32 [units][128 rows][D] (unnormalised,
+// relative to the chunk's m), then (m, l) float2 [units][128 rows].
+__host__ __device__ constexpr int64_t ws_ml_offset(int64_t units, int D) { return units * ATT_BM * D; }
+__host__ __device__ constexpr int64_t ws_bytes(int64_t units, int D) { return units * ATT_BM * (D + 2) * 4; }
+
 template <int D, bool CAUSAL, int OUT_DT>
 __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ qs, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
-    int Sq, int Skv, int Skp, int q_tiles, int total, float c0) {
+    int Sq, int Skv, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part, float c0) {
   constexpr int BN = ATT_BN;
   constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
   constexpr int VTILE = D * BN;      // bytes of the V tile  ([D channels][64 keys])
@@ -62,8 +69,16 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   constexpr int VLOADS = VTILE / 1024 / 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][TILE];
 
-  // ---- work decode ----
-  const int logical = xcd_remap(blockIdx.x, total);
+  // ---- work decode: blocks [0, n_full) own whole query tiles (XCD-grouped); each later block owns one of the
+  // `chunks` key ranges of a split tile ----
+  const bool split = (int)blockIdx.x >= n_full;
+  int logical, unit = 0;
+  if (!split) {
+    logical = xcd_remap(blockIdx.x, n_full);
+  } else {
+    unit = blockIdx.x - n_full;
+    logical = n_full + unit / chunks;
+  }
   const int bh = logical / q_tiles;
   int qt = logical % q_tiles;
   if (CAUSAL) qt = q_tiles - 1 - qt;  // longest rows first within a head
@@ -72,7 +87,7 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   const int bhk = b * Hkv + hkv;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, hf = lane >> 5;
   const int q0 = qt * ATT_BM + wave * 32;
   const int qrow = q0 + ln;
@@ -93,6 +108,12 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   int kv_end = Skv;
   if (CAUSAL) kv_end = min(Skv, qt * ATT_BM + ATT_BM + off);
   const int ntiles = (kv_end + BN - 1) / BN;
+  int t_lo = 0, t_hi = ntiles;
+  if (split) {
+    const int ch = unit % chunks;
+    t_lo = ch * ntiles / chunks;
+    t_hi = (ch + 1) * ntiles / chunks;
+  }
 
   const int8_t* kbase = k8 + (int64_t)bhk * Skp * D;
   const uint8_t* vbase = v8t + (int64_t)bhk * D * Skp;
@@ -100,28 +121,37 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
 
   // Source of each lane's direct loads.  Load j of wave w fills LDS chunk L = (w * LOADS + j) * 64 + lane of the
   // region, which must receive the tile chunk that the swizzled layout stores there.
-  int koff[KLOADS];
-  int64_t voff[VLOADS];
+  uint32_t koff[KLOADS];
+  uint32_t voff[VLOADS];  // D * Skp < 2^31 (checked on the host)
 #pragma unroll
   for (int j = 0; j < KLOADS; ++j) {
     const int L = (wave * KLOADS + j) * 64 + lane;
     const int row = L / KCH;
-    koff[j] = row * D + swz<D>(row, L % KCH) * 16;  // swz is an involution: stored chunk c' holds chunk c' ^ s
+    koff[j] = (uint32_t)(row * D + swz<D>(row, L % KCH) * 16);  // swz is an involution: stored chunk c' holds chunk c' ^ s
   }
 #pragma unroll
   for (int j = 0; j < VLOADS; ++j) {
     const int L = (wave * VLOADS + j) * 64 + lane;
     const int d = L >> 2;
-    voff[j] = (int64_t)d * Skp + swz<BN>(d, L & 3) * 16;
+    voff[j] = (uint32_t)(d * Skp + swz<BN>(d, L & 3) * 16);
   }
 #define SAGE_ISSUE_TILE(T, BUF)                                                                            \
   do {                                                                                                     \
     const int tt_ = (T);                                                                                   \
     uint8_t* dst_ = smem[BUF];                                                                             \
-    _Pragma("unroll") for (int j_ = 0; j_ < KLOADS; ++j_)                                                  \
-      copy16_to_lds(kbase + (int64_t)tt_ * KTILE + koff[j_], dst_ + (wave * KLOADS + j_) * 1024);          \
-    _Pragma("unroll") for (int j_ = 0; j_ < VLOADS; ++j_)                                                  \
-      copy16_to_lds(vbase + voff[j_] + tt_ * BN, dst_ + KTILE + (wave * VLOADS + j_) * 1024);              \
+    /* uniform bases pinned to SGPRs and offsets widened here (not hoisted as 64-bit values): each load is    \
+       then the SGPR-pair base + 32-bit lane offset form, with no 64-bit address registers */                \
+    const int8_t* kb_ = kbase + (int64_t)tt_ * KTILE;                                                      \
+    const uint8_t* vb_ = vbase + tt_ * BN;                                                                 \
+    asm volatile("" : "+s"(kb_), "+s"(vb_));                                                               \
+    _Pragma("unroll") for (int j_ = 0; j_ < KLOADS; ++j_) {                                                \
+      asm volatile("" : "+v"(koff[j_]));                                                                 \
+      copy16_to_lds(kb_ + koff[j_], dst_ + (wave * KLOADS + j_) * 1024);                                    \
+    }                                                                                                      \
+    _Pragma("unroll") for (int j_ = 0; j_ < VLOADS; ++j_) {                                                \
+      asm volatile("" : "+v"(voff[j_]));                                                                 \
+      copy16_to_lds(vb_ + voff[j_], dst_ + KTILE + (wave * VLOADS + j_) * 1024);                            \
+    }                                                                                                      \
   } while (0)
 
   // Lane-constant LDS offsets of the MFMA operands.  For rows 32 kb + ln the K swizzle does not depend on kb, and
@@ -212,20 +242,20 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   // are asynchronous writes to LDS the compiler does not track, hence the explicit vmcnt waits before barriers.
   int t_mask = Skv / BN;
   if (CAUSAL) t_mask = min(t_mask, max(0, (q0 + off + 1) / BN));
-  t_mask = min(t_mask, ntiles);
+  t_mask = min(t_mask, t_hi);
   const v16i zero16 = {};
-  SAGE_ISSUE_TILE(0, 0);
+  SAGE_ISSUE_TILE(t_lo, t_lo & 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  int t = 0;
+  int t = t_lo;
   for (; t < t_mask; ++t) {
-    if (t + 1 < ntiles) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+    if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
     SAGE_TILE(t, false);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
-  for (; t < ntiles; ++t) {
-    if (t + 1 < ntiles) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+  for (; t < t_hi; ++t) {
+    if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
     SAGE_TILE(t, true);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -235,6 +265,20 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
 
   // ---- epilogue ----
   const float lt = l + xor32_f32(l);
+  if (split) {
+    // partial state of this key range (workspace layout at ws_ml_offset), merged by attn_merge_kernel
+    const int q = wave * 32 + ln;
+    float* po = part + ((int64_t)unit * ATT_BM + q) * D;
+#pragma unroll
+    for (int i = 0; i < NPV; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(po + 32 * i + 8 * g + 4 * hf) =
+            make_float4(o[i][4 * g + 0], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
+    const int64_t units = (int64_t)(total - n_full) * chunks;
+    if (hf == 0) reinterpret_cast<float2*>(part + ws_ml_offset(units, D))[(int64_t)unit * ATT_BM + q] = make_float2(m, lt);
+    return;
+  }
   const float inv = (1.0f / 448.0f) / lt;
   if (qvalid) {
     uint16_t* orow = out + b * osb + (int64_t)qrow * oss + h * osh;
@@ -259,54 +303,228 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Merge of split tiles: one thread per (split tile s, row r, 4-channel group c), consecutive threads on consecutive
+// groups of a row, so partial reads and output writes are contiguous; every partial load of a thread is issued before
+// the first is used.  With M = max_i m_i over the chunks, w_i = 2^((m_i - M) * cl), L = sum_i w_i l_i and
+// O = sum_i w_i O_i (float32, chunk order), the output is (O * ((1/448) / L)) * VS and lse = ln2 * (cl * M + log2 L),
+// the epilogue of an unsplit tile.  grid = n_split * 128 * (D / 4) / 256 blocks of 256 threads.
+// ------------------------------------------------------------------------------------------------------------------
+template <int D, int OUT_DT>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qs,
+                                                         const float* __restrict__ vs, uint16_t* __restrict__ out,
+                                                         int64_t osb, int64_t oss, int64_t osh,
+                                                         float* __restrict__ lse, int H, int Hkv, int Sq, int q_tiles,
+                                                         int n_full, int n_split, int chunks, float c0) {
+  constexpr int NG = D / 4;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int cg = idx % NG;
+  const int q = (idx / NG) % ATT_BM;
+  const int s = idx / (NG * ATT_BM);
+  const int logical = n_full + s;
+  const int bh = logical / q_tiles, qt = logical % q_tiles;
+  const int qrow = qt * ATT_BM + q;
+  if (qrow >= Sq) return;
+  const int b = bh / H, h = bh % H;
+  const int bhk = b * Hkv + h / (H / Hkv);
+  const int64_t units = (int64_t)n_split * chunks, unit0 = (int64_t)s * chunks;
+  const float2* ml = reinterpret_cast<const float2*>(part + ws_ml_offset(units, D)) + unit0 * ATT_BM + q;
+  const float* po = part + (unit0 * ATT_BM + q) * D + 4 * cg;
+  float2 e[ATT_MAX_CHUNKS];
+  float4 oi[ATT_MAX_CHUNKS];
+#pragma unroll
+  for (int i = 0; i < ATT_MAX_CHUNKS; ++i) {
+    if (i < chunks) {
+      e[i] = ml[i * ATT_BM];
+      oi[i] = *reinterpret_cast<const float4*>(po + (int64_t)i * ATT_BM * D);
+    }
+  }
+  const float cl = c0 * qs[(int64_t)bh * Sq + qrow];
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < ATT_MAX_CHUNKS; ++i)
+    if (i < chunks) M = fmaxf(M, e[i].x);
+  float L = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int i = 0; i < ATT_MAX_CHUNKS; ++i) {
+    if (i < chunks) {
+      const float w = __builtin_amdgcn_exp2f((e[i].x - M) * cl);
+      L = L + w * e[i].y;
+      acc.x = acc.x + w * oi[i].x;
+      acc.y = acc.y + w * oi[i].y;
+      acc.z = acc.z + w * oi[i].z;
+      acc.w = acc.w + w * oi[i].w;
+    }
+  }
+  const float inv = (1.0f / 448.0f) / L;
+  const v4f sc4 = *reinterpret_cast<const v4f*>(vs + (int64_t)bhk * D + 4 * cg);
+  const uint32_t e0 = f32_to_out_bits<OUT_DT>((acc.x * inv) * sc4[0]);
+  const uint32_t e1 = f32_to_out_bits<OUT_DT>((acc.y * inv) * sc4[1]);
+  const uint32_t e2 = f32_to_out_bits<OUT_DT>((acc.z * inv) * sc4[2]);
+  const uint32_t e3 = f32_to_out_bits<OUT_DT>((acc.w * inv) * sc4[3]);
+  uint16_t* orow = out + b * osb + (int64_t)qrow * oss + h * osh;
+  *reinterpret_cast<uint2*>(orow + 4 * cg) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+  if (lse != nullptr && cg == 0) lse[(int64_t)bh * Sq + qrow] = 0.69314718055994531f * (cl * M + __log2f(L));
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Work plan.  A launch of n_tiles query tiles runs in rounds of `slots` = CUs x resident workgroups per CU.  When the
+// last round is short (rem = n_tiles mod slots tiles), its tiles run at a fraction of the chip's throughput: the
+// plan splits the key range of those rem tiles into chunks = slots / rem parts (at most 16, at least 4 key tiles
+// each) so that the last round fills the chip again, and a merge kernel combines the parts.  Causal tiles are
+// never split.
+// ------------------------------------------------------------------------------------------------------------------
+struct AttnPlan {
+  int n_tiles, n_full, chunks;
+  int64_t workspace;  // bytes of partial state
+};
+
+static int device_cus(int* cus) {
+  static int cache[64] = {0};
+  int dev = 0;
+  SAGE_HIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) {
+    *cus = cache[dev];
+    return SAGE_OK;
+  }
+  int n = 0;
+  SAGE_HIP_CHECK(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  *cus = n;
+  return SAGE_OK;
+}
+
 template <int D, bool CAUSAL, int OUT_DT>
-static void launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
-                        const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, float* lse, int B, int H,
-                        int Hkv, int Sq, int Skv, hipStream_t st) {
+static int resident_blocks(int* per_cu) {
+  static int cache = 0;
+  if (cache == 0) {
+    int n = 0;
+    SAGE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<D, CAUSAL, OUT_DT>, ATT_THREADS, 0),
+                   "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    cache = n;
+  }
+  *per_cu = cache;
+  return SAGE_OK;
+}
+
+template <int D, bool CAUSAL, int OUT_DT>
+static int make_plan(int B, int H, int Sq, int Skv, AttnPlan* p) {
   const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
-  const int total = B * H * q_tiles;
+  p->n_tiles = B * H * q_tiles;
+  p->n_full = p->n_tiles;
+  p->chunks = 1;
+  p->workspace = 0;
+  if (CAUSAL) return SAGE_OK;
+  int cus = 0, per_cu = 0, rc;
+  if ((rc = device_cus(&cus))) return rc;
+  if ((rc = resident_blocks<D, CAUSAL, OUT_DT>(&per_cu))) return rc;
+  const int slots = cus * per_cu;
+  if (slots <= 0) return SAGE_OK;
+  const int rem = p->n_tiles % slots;
+  if (rem == 0) return SAGE_OK;
+  const int kv_tiles = (Skv + ATT_BN - 1) / ATT_BN;
+  const int chunks = min(min(slots / rem, kv_tiles / 4), ATT_MAX_CHUNKS);
+  if (chunks < 2) return SAGE_OK;
+  p->n_full = p->n_tiles - rem;
+  p->chunks = chunks;
+  p->workspace = ws_bytes((int64_t)rem * chunks, D);
+  return SAGE_OK;
+}
+
+template <int D, bool CAUSAL, int OUT_DT>
+static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
+                       const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, float* lse, int B, int H,
+                       int Hkv, int Sq, int Skv, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  AttnPlan p;
+  int rc;
+  if (workspace == nullptr) {
+    const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
+    p.n_tiles = p.n_full = B * H * q_tiles;
+    p.chunks = 1;
+    p.workspace = 0;
+  } else {
+    if ((rc = make_plan<D, CAUSAL, OUT_DT>(B, H, Sq, Skv, &p))) return rc;
+    SAGE_REQUIRE(workspace_bytes >= p.workspace, "sage_attn_fwd: workspace of %lld bytes, the plan needs %lld",
+                 (long long)workspace_bytes, (long long)p.workspace);
+    SAGE_REQUIRE(((uintptr_t)workspace & 255u) == 0, "sage_attn_fwd: workspace must be 256-byte aligned");
+  }
+  const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
+  const int n_split = p.n_tiles - p.n_full;
+  const int blocks = p.n_full + n_split * p.chunks;
   const float c0 = (float)((1.0 / __builtin_sqrt((double)D)) * 1.4426950408889634);
-  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT>), dim3(total), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t, vs,
-                     static_cast<uint16_t*>(out), osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, total, c0);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  float* part = static_cast<float*>(workspace);
+  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t, vs,
+                     o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks, part,
+                     c0);
+  if (n_split > 0) {
+    if ((rc = check_launch("attention launch"))) return rc;
+    hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
+                       part, qs, vs, o, osb, oss, osh, lse, H, Hkv, Sq, q_tiles, p.n_full, n_split, p.chunks, c0);
+  }
+  return check_launch("attention launch");
+}
+
+static int check_attn_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, const char* who) {
+  SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "%s: sizes must be positive", who);
+  SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
+  if (D != 64 && D != 128) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 128)", who, D);
+  if (causal && Sq != Skv) return fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len == kv_len", who);
+  SAGE_REQUIRE((int64_t)B * H * ((Sq + ATT_BM - 1) / ATT_BM) * ATT_MAX_CHUNKS < (1ll << 31), "%s: too many query tiles",
+               who);
+  SAGE_REQUIRE((int64_t)D * kv_pad(Skv) < (1ll << 31), "%s: kv_len %d too long", who, Skv);
+  return SAGE_OK;
+}
+
+#define SAGE_ATTN_DISPATCH(D, CAUSAL, BF, FN, ...)                               \
+  ((D) == 128 ? ((CAUSAL) ? ((BF) ? FN<128, true, DT_BF16>(__VA_ARGS__) : FN<128, true, DT_F16>(__VA_ARGS__))  \
+                          : ((BF) ? FN<128, false, DT_BF16>(__VA_ARGS__) : FN<128, false, DT_F16>(__VA_ARGS__))) \
+              : ((CAUSAL) ? ((BF) ? FN<64, true, DT_BF16>(__VA_ARGS__) : FN<64, true, DT_F16>(__VA_ARGS__))    \
+                          : ((BF) ? FN<64, false, DT_BF16>(__VA_ARGS__) : FN<64, false, DT_F16>(__VA_ARGS__))))
+
+int attn_plan_impl(int B, int H, int Sq, int Skv, int D, int causal, int* n_full, int* chunks, int64_t* ws) {
+  int rc = check_attn_shape(B, H, H, Sq, Skv, D, causal, "sage_attn_plan");
+  if (rc) return rc;
+  AttnPlan p;
+  // the plan depends on the kernel's occupancy, which is the same for both output dtypes
+  if ((rc = SAGE_ATTN_DISPATCH(D, causal, true, make_plan, B, H, Sq, Skv, &p))) return rc;
+  if (n_full) *n_full = p.n_full;
+  if (chunks) *chunks = p.chunks;
+  if (ws) *ws = p.workspace;
+  return SAGE_OK;
 }
 
 int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t, const float* vs,
               void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D,
-              int causal, int out_dtype, float* lse, void* stream) {
+              int causal, int out_dtype, float* lse, void* workspace, int64_t workspace_bytes, void* stream) {
   const char* who = "sage_attn_fwd";
-  SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "%s: sizes must be positive", who);
-  SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
-  if (D != 64 && D != 128) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 128)", who, D);
+  int rc = check_attn_shape(B, H, Hkv, Sq, Skv, D, causal, who);
+  if (rc) return rc;
   if (out_dtype != SAGE_DTYPE_BF16 && out_dtype != SAGE_DTYPE_F16)
     return fail(SAGE_ERR_UNSUPPORTED, "%s: out dtype code %d", who, out_dtype);
-  if (causal && Sq != Skv) return fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len == kv_len", who);
   SAGE_REQUIRE(q8 && qs && k8 && ks && v8t && vs && out, "%s: a pointer argument is NULL", who);
   SAGE_REQUIRE(aligned16(q8) && aligned16(k8) && aligned16(v8t) && aligned16(vs) && aligned16(out),
                "%s: q8 / k8 / v8t / vs / out must be 16-byte aligned", who);
   SAGE_REQUIRE(osb % 8 == 0 && oss % 8 == 0 && osh % 8 == 0 && osb >= 0 && oss >= 0 && osh >= 0,
                "%s: out strides must be non-negative multiples of 8 elements", who);
-  SAGE_REQUIRE((int64_t)B * H * ((Sq + ATT_BM - 1) / ATT_BM) < (1ll << 31), "%s: too many query tiles", who);
-  hipStream_t st = (hipStream_t)stream;
-#define SAGE_ATTN_CASE(DD, CC, OO) \
-  launch_attn<DD, CC, OO>(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, lse, B, H, Hkv, Sq, Skv, st)
-  const bool bf = out_dtype == SAGE_DTYPE_BF16;
-  if (D == 128) {
-    if (causal) { if (bf) SAGE_ATTN_CASE(128, true, DT_BF16); else SAGE_ATTN_CASE(128, true, DT_F16); }
-    else { if (bf) SAGE_ATTN_CASE(128, false, DT_BF16); else SAGE_ATTN_CASE(128, false, DT_F16); }
-  } else {
-    if (causal) { if (bf) SAGE_ATTN_CASE(64, true, DT_BF16); else SAGE_ATTN_CASE(64, true, DT_F16); }
-    else { if (bf) SAGE_ATTN_CASE(64, false, DT_BF16); else SAGE_ATTN_CASE(64, false, DT_F16); }
-  }
-#undef SAGE_ATTN_CASE
-  return check_launch("attention launch");
+  return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn, q8, qs, k8, ks, v8t, vs, out, osb,
+                            oss, osh, lse, B, H, Hkv, Sq, Skv, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // namespace sage
 
+extern "C" int sage_attn_plan(int B, int H, int Sq, int Skv, int D, int causal, int* n_full, int* chunks,
+                              int64_t* workspace_bytes) {
+  sage::clear_error();
+  return sage::attn_plan_impl(B, H, Sq, Skv, D, causal, n_full, chunks, workspace_bytes);
+}
+
 extern "C" int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
                              const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv,
-                             int Sq, int Skv, int D, int causal, int out_dtype, float* lse, void* stream) {
+                             int Sq, int Skv, int D, int causal, int out_dtype, float* lse, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
   sage::clear_error();
   return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, out_dtype, lse,
-                         stream);
+                         workspace, workspace_bytes, stream);
 }

@@ -28,13 +28,14 @@ int v_amax_impl(const void*, int64_t, int64_t, int64_t, int, int, int, int, int,
 int quant_kv_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, int, int, int, int,
                   int, const float*, int8_t*, float*, uint8_t*, void*);
 int attn_impl(const int8_t*, const float*, const int8_t*, const float*, const uint8_t*, const float*, void*, int64_t,
-              int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*);
+              int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*, int64_t, void*);
+int attn_plan_impl(int, int, int, int, int, int, int*, int*, int64_t*);
 
 }  // namespace sage
 
 extern "C" {
 
-int sage_abi_version(void) { return 1; }
+int sage_abi_version(void) { return 2; }
 
 const char* sage_last_error(void) { return sage::g_err; }
 
@@ -46,28 +47,43 @@ const char* sage_manifest_json(void) {
          "\"quant_q\": {\"rows_per_block\": 64, \"threads\": 256, \"lanes_per_row\": 4, \"rotation\": \"fwht_f64\"}, "
          "\"quant_kv\": {\"rows_per_block\": 128, \"threads\": 256}, "
          "\"v_amax\": {\"rows_per_block\": 256, \"threads\": 256}, "
-         "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": 2, "
+         "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": 3, \"max_kv_chunks\": 16, "
          "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
          "\"variants\": [\"d64\", \"d128\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}}";
+}
+
+int sage_forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* workspace_bytes) {
+  sage::clear_error();
+  SAGE_REQUIRE(workspace_bytes != nullptr, "sage_forward_workspace: workspace_bytes is NULL");
+  SAGE_REQUIRE(Hkv > 0 && H % Hkv == 0, "sage_forward_workspace: heads %d not a multiple of kv heads %d", H, Hkv);
+  return sage::attn_plan_impl(B, H, Sq, Skv, D, causal, nullptr, nullptr, workspace_bytes);
 }
 
 int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                  int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb, int64_t oss,
                  int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float qs_mul,
-                 int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* stream) {
+                 int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace,
+                 int64_t workspace_bytes, void* stream) {
   sage::clear_error();
   // validate everything before the first launch so a bad call leaves the stream untouched
   SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "sage_forward: sizes must be positive");
   SAGE_REQUIRE(H % Hkv == 0, "sage_forward: heads %d not a multiple of kv heads %d", H, Hkv);
   if (D != 64 && D != 128) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 128)", D);
   if (causal && Sq != Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len == kv_len");
+  if (workspace != nullptr) {
+    int64_t need = 0;
+    int rc0 = sage::attn_plan_impl(B, H, Sq, Skv, D, causal, nullptr, nullptr, &need);
+    if (rc0) return rc0;
+    SAGE_REQUIRE(workspace_bytes >= need, "sage_forward: workspace of %lld bytes, the plan needs %lld",
+                 (long long)workspace_bytes, (long long)need);
+  }
   int rc;
   if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;
   if ((rc = sage::quant_q_impl(q, qsb, qss, qsh, B, H, Sq, D, dtype, qs_mul, q8, qs, stream))) return rc;
   if ((rc = sage::quant_kv_impl(k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, k8, ks, v8t, stream)))
     return rc;
   return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype, nullptr,
-                         stream);
+                         workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -5,6 +5,7 @@ import numpy as np
 import torch
 
 from cdna4_sage import _capi
+from oracle import sage_oracle as orc
 
 DT = {torch.bfloat16: _capi.DTYPE_BF16, torch.float16: _capi.DTYPE_F16}
 
@@ -64,3 +65,12 @@ def cosine(a, b) -> float:
     a = np.asarray(a, dtype=np.float64).ravel()
     b = np.asarray(b, dtype=np.float64).ravel()
     return float((a * b).sum() / np.sqrt((a * a).sum() * (b * b).sum()))
+
+
+def kv_split(dev, B, H, Sq, Skv, D, causal, heads=None):
+    """The emulation's ``kv_split`` argument that follows the attention kernel's plan on `dev` (None when the plan
+    splits nothing).  ``heads``: indices, in the full problem of H heads, of the heads an emulated sample holds."""
+    n_full, chunks, _ = _capi.attn_plan(torch.device(dev).index or 0, B, H, Sq, Skv, D, bool(causal))
+    if chunks <= 1:
+        return None
+    return chunks, orc.split_rows(B, H, Sq, n_full, heads=heads)

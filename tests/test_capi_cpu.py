@@ -68,7 +68,7 @@ def test_kv_and_attention_validation():
     assert lib.sage_quant_kv(P, 0, 128, 0, P, 0, 128, 0, 1, 1, 64, 128, 0, P, P, P, P + 8, None) == _capi.SAGE_ERR_INVALID
     assert "16-byte" in _err()
     args = dict(q8=P, qs=P, k8=P, ks=P, v8t=P, vs=P, out=P, osb=0, oss=128, osh=128, B=1, H=4, Hkv=2, Sq=64, Skv=64,
-                D=128, causal=0, out_dtype=0, lse=None, stream=None)
+                D=128, causal=0, out_dtype=0, lse=None, workspace=None, workspace_bytes=0, stream=None)
 
     def attn(**kw):
         a = dict(args, **kw)
@@ -81,12 +81,21 @@ def test_kv_and_attention_validation():
     assert attn(q8=None) == _capi.SAGE_ERR_INVALID
     assert attn(oss=100) == _capi.SAGE_ERR_INVALID
     assert attn(Sq=0) == _capi.SAGE_ERR_INVALID
+    n_full, chunks, ws = ctypes.c_int(-1), ctypes.c_int(-1), ctypes.c_int64(-1)
+    refs = (ctypes.byref(n_full), ctypes.byref(chunks), ctypes.byref(ws))
+    assert lib.sage_attn_plan(1, 4, 64, 64, 96, 0, *refs) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 96" in _err()
+    assert lib.sage_attn_plan(1, 4, 64, 65, 128, 1, *refs) == _capi.SAGE_ERR_UNSUPPORTED
+    assert lib.sage_attn_plan(0, 4, 64, 64, 128, 0, *refs) == _capi.SAGE_ERR_INVALID
+    assert (n_full.value, chunks.value, ws.value) == (-1, -1, -1)       # outputs untouched on error
+    wsb = ctypes.c_int64(-1)
+    assert lib.sage_forward_workspace(1, 4, 3, 64, 64, 128, 0, ctypes.byref(wsb)) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_forward_workspace(1, 4, 2, 64, 64, 128, 0, None) == _capi.SAGE_ERR_INVALID
 
 
 def test_forward_validates_before_launching_and_python_raises():
     lib = _capi.lib()
     rc = lib.sage_forward(P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128, 1, 4, 2, 64, 80, 128, 0, 1, 1.0,
-                          P, P, P, P, P, P, None)
+                          P, P, P, P, P, P, None, 0, None)
     assert rc == _capi.SAGE_ERR_UNSUPPORTED and "causal" in _err()
     with pytest.raises(_capi.SageError, match="head_dim 80"):
         _capi.call("sage_quant_q", P, 0, 128, 0, 1, 1, 64, 80, 0, 1.0, P, P, None)

@@ -10,7 +10,7 @@ import torch.nn.functional as F
 
 import cdna4_sage
 from cdna4_sage import _capi
-from gpu_util import cosine, hnd_np
+from gpu_util import cosine, hnd_np, kv_split
 from oracle import sage_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -40,11 +40,13 @@ def _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=0):
     return q, k, v
 
 
-def _emulate(q, k, v, layout, causal, sm_scale=None, out_dtype="bf16"):
+def _emulate(q, k, v, layout, causal, sm_scale=None, out_dtype="bf16", split=None):
+    """Emulation at the kernel's 64-key tile, following the kernel's split plan (`split`, from gpu_util.kv_split)."""
     qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
     q8, qs = orc.quant_q(qn, sm_scale)
     k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(kn.shape[2]))
-    emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=64, out_dtype=out_dtype)
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=64, out_dtype=out_dtype,
+                        kv_split=split)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, sm_scale=sm_scale)
     return emu, ref
 
@@ -55,7 +57,8 @@ def test_attention_vs_emulation(dev, B, H, Hkv, Sq, Skv, D, dt, layout, causal):
     out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), tensor_layout=layout, is_causal=causal)
     assert out.shape == q.shape and out.dtype == dt
     got = hnd_np(out, layout)
-    emu, ref = _emulate(q, k, v, layout, causal, out_dtype="bf16" if dt == torch.bfloat16 else "f16")
+    split = kv_split(dev, B, H, Sq, Skv, D, causal)
+    emu, ref = _emulate(q, k, v, layout, causal, out_dtype="bf16" if dt == torch.bfloat16 else "f16", split=split)
     err = float(np.abs(got - emu).max())
     c = cosine(got, ref)
     assert err <= MAX_ABS, err
@@ -65,7 +68,7 @@ def test_attention_vs_emulation(dev, B, H, Hkv, Sq, Skv, D, dt, layout, causal):
 def test_sm_scale(dev):
     q, k, v = _inputs(1, 2, 2, 600, 600, 128, torch.bfloat16, "HND", seed=7)
     out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), "HND", sm_scale=0.05)
-    emu, ref = _emulate(q, k, v, "HND", False, sm_scale=0.05)
+    emu, ref = _emulate(q, k, v, "HND", False, sm_scale=0.05, split=kv_split(dev, 1, 2, 600, 600, 128, False))
     got = hnd_np(out)
     assert float(np.abs(got - emu).max()) <= MAX_ABS
     assert cosine(got, ref) >= COS
@@ -73,7 +76,9 @@ def test_sm_scale(dev):
 
 def test_flux_config2_full(dev):
     """Config 2 (Flux 1x24x4608x128 bf16, outlier K channels): cosine vs fp32 attention on all heads, and the
-    emulation on a two-head sample (the per-head computation is independent of the other heads)."""
+    emulation on a two-head sample (the per-head computation is independent of the other heads).  Heads 21 and 22
+    hold the tiles of the short last round, which the kernel's plan splits on a 256-CU device: the sample covers
+    whole and split tiles."""
     from cdna4_sage.configs import CONFIGS, make_inputs
 
     cfg = CONFIGS["2"]
@@ -82,10 +87,60 @@ def test_flux_config2_full(dev):
     ref = F.scaled_dot_product_attention(q.to(dev).float(), k.to(dev).float(), v.to(dev).float())
     c = F.cosine_similarity(out.float().flatten(), ref.flatten(), dim=0).item()
     assert c >= COS, c
-    qs_, ks_, vs_ = make_inputs(cfg, heads=slice(5, 7))
-    emu, _ = _emulate(qs_, ks_, vs_, "HND", False)
-    got = out[:, 5:7].float().cpu().numpy()
+    qs_, ks_, vs_ = make_inputs(cfg, heads=slice(21, 23))
+    split = kv_split(dev, cfg.B, cfg.H, cfg.S, cfg.S, cfg.D, False, heads=[21, 22])
+    emu, _ = _emulate(qs_, ks_, vs_, "HND", False, split=split)
+    got = out[:, 21:23].float().cpu().numpy()
     assert float(np.abs(got - emu).max()) <= MAX_ABS
+
+
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 600, 600, 128), (2, 4, 515, 515, 64), (3, 2, 77, 1031, 128)])
+def test_split_plan_and_unsplit_call(dev, B, H, Sq, Skv, D):
+    """Small problems fill one partial round, so the plan splits their key range; a call without workspace runs
+    every tile whole and must match the unsplit emulation, the default call the split one."""
+    n_full, chunks, ws = _capi.attn_plan(dev.index or 0, B, H, Sq, Skv, D, False)
+    n_split = B * H * ((Sq + 127) // 128)
+    # fp32 O partials and (m, l) per row of each chunk
+    assert n_full == 0 and chunks >= 2 and ws == n_split * chunks * 128 * (D + 2) * 4
+    q, k, v = _inputs(B, H, H, Sq, Skv, D, torch.bfloat16, "HND", seed=B + Sq)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    from gpu_util import run_quant_kv, run_quant_q
+    q8, qs = (torch.from_numpy(a).to(dev) for a in run_quant_q(qd))
+    k8, ks, v8t, vs = (torch.from_numpy(a).to(dev) for a in run_quant_kv(kd, vd))
+    st = torch.cuda.current_stream(dev).cuda_stream
+    outs = []
+    for wsz in (0, ws):
+        out = torch.empty(B, H, Sq, D, device=dev, dtype=torch.bfloat16)
+        buf = torch.empty(max(wsz, 1), device=dev, dtype=torch.uint8)
+        _capi.call("sage_attn_fwd", q8.data_ptr(), qs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(),
+                   vs.data_ptr(), out.data_ptr(), out.stride(0), out.stride(2), out.stride(1), B, H, H, Sq, Skv, D,
+                   0, _capi.DTYPE_BF16, None, buf.data_ptr() if wsz else None, wsz, st)
+        outs.append(out.float().cpu().numpy())
+    with pytest.raises(_capi.SageError, match="workspace"):
+        _capi.call("sage_attn_fwd", q8.data_ptr(), qs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(),
+                   vs.data_ptr(), out.data_ptr(), out.stride(0), out.stride(2), out.stride(1), B, H, H, Sq, Skv, D,
+                   0, _capi.DTYPE_BF16, None, buf.data_ptr(), ws - 1, st)
+    whole, _ = _emulate(q, k, v, "HND", False)
+    split, ref = _emulate(q, k, v, "HND", False, split=(chunks, np.ones((B, H, Sq), dtype=bool)))
+    assert float(np.abs(outs[0] - whole).max()) <= MAX_ABS
+    assert float(np.abs(outs[1] - split).max()) <= MAX_ABS
+    assert cosine(outs[1], ref) >= COS
+
+
+def test_split_merge_is_deterministic_across_calls(dev):
+    """Split tiles are merged from partials in a workspace that every call reuses.  Repeated calls that alternate
+    two inputs must reproduce each output bit for bit: a merge that read stale partials of the previous call, or
+    depended on the order in which chunks finished, would not."""
+    from cdna4_sage.configs import CONFIGS, make_inputs
+
+    cfg = CONFIGS["2"]
+    a = [t.to(dev) for t in make_inputs(cfg)]
+    b = [t.flip(2).contiguous() for t in a]
+    outs = [cdna4_sage.attention(*(a if i % 2 == 0 else b), "HND").clone() for i in range(6)]
+    torch.cuda.synchronize()
+    for i in range(2, 6):
+        assert torch.equal(outs[i], outs[i % 2]), i
+    assert not torch.equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("D", [96, 256])

@@ -237,6 +237,51 @@ def test_emulation_softmax_bookkeeping_gives_exact_lse():
         assert np.allclose(lse2, exact, rtol=0, atol=2e-5), bn
 
 
+def test_split_emulation_gives_exact_lse_and_matches_unsplit():
+    """Split-key-range merge (the gfx950 kernel's tail tiles): the merged (M, L) must still give the exact
+    logsumexp (a wrong merge weight or sign fails), one chunk must equal the unsplit emulation bit for bit, and the
+    merged output must stay as close to float64 attention as the unsplit one."""
+    q, k, v = _bf16((1, 2, 64, 128), 18), _bf16((1, 2, 300, 128), 19, 2.0), _bf16((1, 2, 300, 128), 20)
+    k[:, :, 100:140] *= 8.0
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    rows = np.ones((1, 2, 64), dtype=bool)
+    rows[:, 1, 32:] = False                       # unsplit rows must come back untouched
+    base, m0, l0 = orc.attention(q8, qs, k8, ks, v8, vs, 300, block_n=64, out_dtype="f32", return_stats=True)
+    one = orc.attention(q8, qs, k8, ks, v8, vs, 300, block_n=64, out_dtype="f32", kv_split=(1, rows))
+    assert np.array_equal(one, base)
+    cl = orc.logit_scale_base(128) * qs
+    ksr = np.repeat(ks, 32, axis=-1)[:, :, :300]
+    s = np.einsum("bhqd,bhkd->bhqk", q8.astype(np.float64), k8[:, :, :300].astype(np.float64))
+    logit2 = s * cl[..., None].astype(np.float64) * ksr[:, :, None, :]
+    mx = logit2.max(-1)
+    exact = mx + np.log2(np.exp2(logit2 - mx[..., None]).sum(-1))
+    ref = orc.sdpa_reference(q, k, v)
+    for chunks in (2, 3, 5):
+        out, m, l = orc.attention(q8, qs, k8, ks, v8, vs, 300, block_n=64, out_dtype="f32", return_stats=True,
+                                  kv_split=(chunks, rows))
+        lse2 = cl.astype(np.float64) * m + np.log2(l.astype(np.float64))
+        assert np.allclose(lse2, exact, rtol=0, atol=2e-5), chunks
+        assert np.array_equal(out[~rows], base[~rows]) and np.array_equal(m[~rows], m0[~rows])
+        # the split keeps small probabilities that an unsplit tile flushes in E4M3, so it is compared with float64
+        # attention, not with the unsplit emulation
+        assert _cos(out, ref) >= _cos(base, ref) - 1e-4, chunks
+    # O and L must be merged with the same weights: with V = 1 every output is sum(p8) / sum(p) ~ 1
+    ones = np.ones_like(v)
+    k8, ks, v8, vs = orc.quant_kv(_bf16((1, 2, 300, 128), 19), ones)
+    for chunks in (2, 3, 5):
+        out = orc.attention(q8, qs, k8, ks, v8, vs, 300, block_n=64, out_dtype="f32", kv_split=(chunks, rows))
+        assert np.abs(out - 1.0).max() < 1e-2, chunks
+
+
+def test_split_rows_numbering():
+    r = orc.split_rows(2, 3, 300, n_full=7)          # q_tiles = 3: tile = (b * 3 + h) * 3 + row // 128
+    assert r.shape == (2, 3, 300)
+    assert not r[0, 2, 0] and r[0, 2, 128] and r[1].all()   # tile 6 whole, tile 7 split, batch 1 all split
+    s = orc.split_rows(2, 3, 300, n_full=7, heads=[2])
+    assert np.array_equal(s[:, 0], r[:, 2])
+
+
 def test_emulation_gqa_equals_repeated_heads():
     q, k, v = _bf16((1, 4, 70, 64), 21), _bf16((1, 1, 90, 64), 22), _bf16((1, 1, 90, 64), 23)
     a = orc.sage_forward(q, k, v, block_n=64)
