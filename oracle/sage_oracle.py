@@ -28,7 +28,10 @@ What each function restates (paths relative to the reference checkout):
                         lazy rescale with threshold 8.0 (log2 units), exp2, P cast to E4M3, fp32 PV
                         accumulation, epilogue (O * ((1/448) / l)) * VS.  ``block_n`` is the KV tile of the
                         online softmax: 32 in the reference (kernel_build/compile_attn.py:109), 64 in this
-                        build's gfx950 kernel.
+                        build's gfx950 kernel.  The exponent argument is the gfx950 kernel's
+                        fma(1.5 * 2^23 + S, ct, nk) form, which differs from the reference's S * ct - cl * m by
+                        the rounding of nk (at most 1.5 * ct: S moved by less than 2 units, far below the int8
+                        quantization error of S and the E4M3 step of p).
 * ``lse_reference``     src/sageattention/core.py:36-57 (`_lse`).
 
 All float32 steps are written as float32 numpy operations, which round to nearest even like the GPU's
@@ -47,6 +50,7 @@ KV_BLOCK = 32          # one K scale per 32 keys (kernel_build/build_kernels.py:
 E4M3_MAX = 448.0
 RESCALE_THRESHOLD = 8.0  # make_sage.py:219-225: keep a stale max until it is exceeded by 2^8
 LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
+SEED = 12582912.0      # 1.5 * 2^23: fp32 whose integer-valued neighbours hold int32 QK sums exactly
 
 
 # ----------------------------------------------------------------------------------------------------------
@@ -302,7 +306,13 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
             corr = np.exp2(((m - m_new).astype(F32) * cl).astype(F32)).astype(F32)
         neg = (F32(0.0) - (cl * m_new).astype(F32)).astype(F32)
         ct = (cl[..., None] * kst[:, :, None, :]).astype(F32)    # [B, H, Sq, nsub]
-        arg = (sb.astype(np.float64) * ct[..., None].astype(np.float64) + neg[..., None, None]).astype(F32)
+        # the gfx950 kernel reads S as F = 1.5 * 2^23 + S (exact, |S| < 2^21) and folds the offset into the
+        # additive term: arg = fma(F, ct, nk), nk = neg - fp32(1.5 * 2^23 * ct).  F * ct + nk is exact in float64
+        # (both terms have the magnitude of 1.5 * 2^23 * ct and at most 48 significant bits), so rounding it once
+        # to float32 is the kernel's fma.  It equals S * ct + neg up to the two roundings of nk (<= 1.5 ct).
+        nk = (neg[..., None] - (F32(SEED) * ct).astype(F32)).astype(F32)
+        fs = (sb + F32(SEED)).astype(F32)
+        arg = (fs.astype(np.float64) * ct[..., None].astype(np.float64) + nk[..., None].astype(np.float64)).astype(F32)
         p = np.exp2(arg).astype(F32).reshape(B, H, Sq, block_n)
         tile_sum = p.sum(axis=-1, dtype=F32)
         l = ((corr * l).astype(F32) + tile_sum).astype(F32)

@@ -2,10 +2,13 @@
 //
 // Math (the reference kernel's, kernel_build/make_sage.py:75-107, :196-237; make_sage_r2.py:54-269):
 //   cl_i   = fp32(sm * log2e) * QS_i                      (sm = 1/sqrt(D) baked in; other scales folded into QS)
-//   S_ij   = sum_d Q8_id K8_jd                            (int32, exact)
+//   S_ij   = sum_d Q8_id K8_jd                            (int32, exact; |S| < 2^21)
 //   rowmax = max over the tile's 32-key blocks of (max_j S_ij) * KS_block
 //   lazy rescale: m_cand = max(m, rowmax); need = (m_cand - m) * cl > 8; m_new = need ? m_cand : m
-//   p_ij   = exp2(fma(S_ij, cl * KS_block, -(cl * m_new)))   (<= 2^8, fits E4M3)
+//   p_ij   = exp2(fma(F_ij, ct, nk)) with F_ij = 1.5 * 2^23 + S_ij, ct = cl * KS_block,
+//            nk = -(cl * m_new) - fp32(1.5 * 2^23 * ct)       (<= 2^8, fits E4M3)
+//            The QK accumulators start at the bit pattern of 1.5 * 2^23, so the int32 result read as fp32 is F
+//            exactly and needs no conversion; F * ct + nk equals S * ct - cl * m_new up to the rounding of nk.
 //   l      = corr * l + sum_j p_ij (fp32 p);  O = need ? O * corr : O;  O += e4m3(p) V8
 //   out    = (O * ((1/448) / l)) * VS
 //
@@ -180,12 +183,12 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     _Pragma("unroll") for (int i_ = 0; i_ < NQK; ++i_) {                                                   \
       const v4i k0_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_]);                                         \
       const v4i k1_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_] + 32 * D);                                \
-      s_[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0_, qa[i_], i_ == 0 ? zero16 : s_[0], 0, 0, 0);       \
-      s_[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], i_ == 0 ? zero16 : s_[1], 0, 0, 0);       \
+      s_[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0_, qa[i_], i_ == 0 ? seed16 : s_[0], 0, 0, 0);       \
+      s_[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], i_ == 0 ? seed16 : s_[1], 0, 0, 0);       \
     }                                                                                                      \
     float sf_[2][16];                                                                                      \
     _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
-      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] = (float)s_[kb_][v_];                 \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] = __int_as_float(s_[kb_][v_]);        \
     if (MASKED) {                                                                                          \
       const int kstart_ = t_ * BN;                                                                         \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
@@ -202,20 +205,21 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     mx0_ = fmaxf(mx0_, xor32_f32(mx0_));                                                                   \
     mx1_ = fmaxf(mx1_, xor32_f32(mx1_));                                                                   \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
-    const float rowmax_ = fmaxf(mx0_ * ks0_, mx1_ * ks1_);                                                 \
+    const float rowmax_ = fmaxf((mx0_ - SEED_F) * ks0_, (mx1_ - SEED_F) * ks1_);                           \
     const float mcand_ = fmaxf(m, rowmax_);                                                                \
     const bool need_ = (mcand_ - m) * cl > 8.0f;                                                           \
     const float mnew_ = need_ ? mcand_ : m;                                                                \
     const float corr_ = __builtin_amdgcn_exp2f((m - mnew_) * cl);                                          \
     const float neg_ = 0.0f - cl * mnew_;                                                                  \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
+    const float nk0_ = neg_ - SEED_F * ct0_, nk1_ = neg_ - SEED_F * ct1_;                                  \
     float psum_ = 0.0f;                                                                                    \
     _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
-      sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, neg_));                         \
+      sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, nk0_));                         \
       psum_ += sf_[0][v_];                                                                                 \
     }                                                                                                      \
     _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
-      sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, neg_));                         \
+      sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, nk1_));                         \
       psum_ += sf_[1][v_];                                                                                 \
     }                                                                                                      \
     l = corr_ * l + psum_;                                                                                 \
@@ -243,7 +247,11 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   int t_mask = Skv / BN;
   if (CAUSAL) t_mask = min(t_mask, max(0, (q0 + off + 1) / BN));
   t_mask = min(t_mask, t_hi);
-  const v16i zero16 = {};
+  // QK accumulators start at the bits of 1.5 * 2^23 (0x4B400000): the int32 sum read as fp32 is 1.5 * 2^23 + S
+  constexpr float SEED_F = 12582912.0f;
+  v16i seed16;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) seed16[v] = 0x4B400000;
   SAGE_ISSUE_TILE(t_lo, t_lo & 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();

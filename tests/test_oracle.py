@@ -195,12 +195,19 @@ def test_emulation_vs_float64_attention(block_n, causal):
 
 
 def test_emulation_single_key_returns_dequantized_v():
+    """One key: p = exp2(arg) with arg = 0 up to the two roundings of nk = neg - fp32(1.5 * 2^23 * ct), each at most
+    half an ulp of ~1.5 * 2^23 * ct <= 0.75 * ct.  So out = dequantized V / p with |p - 1| <= 2^(1.5 ct) - 1 (the
+    E4M3 cast of p is exactly 1), and nothing else may perturb it."""
     q, k, v = _bf16((1, 2, 5, 128), 12), _bf16((1, 2, 1, 128), 13), _bf16((1, 2, 1, 128), 14)
     q8, qs = orc.quant_q(q)
     k8, ks, v8, vs = orc.quant_kv(k, v)
     out = orc.attention(q8, qs, k8, ks, v8, vs, 1, out_dtype="f32")
     deq = orc.e4m3_to_f32(v8[:, :, :1]) * vs[:, :, None, :] / 448.0
-    assert np.allclose(out, np.broadcast_to(deq, out.shape), rtol=1e-5, atol=1e-7)
+    ct = orc.logit_scale_base(128).astype(np.float64) * qs * ks[:, :, :1]          # [B, H, Sq]
+    bound = np.exp2(1.51 * ct) - 1.0 + 1e-6
+    rel = np.abs(out / np.broadcast_to(deq, out.shape) - 1.0).max(axis=-1)
+    assert (rel <= bound).all(), (rel.max(), bound.min())
+    assert bound.max() < 1e-3
 
 
 def test_emulation_causal_first_row_and_bottom_right():
@@ -208,7 +215,10 @@ def test_emulation_causal_first_row_and_bottom_right():
     out = orc.sage_forward(q, k, v, causal=True, block_n=32, out_dtype="f32")
     k8, ks, v8, vs = orc.quant_kv(k, v)
     deq0 = orc.e4m3_to_f32(v8[0, 0, 0]) * vs[0, 0] / 448.0
-    assert np.allclose(out[0, 0, 0], deq0, rtol=1e-5, atol=1e-7)     # row 0 sees key 0 only
+    # row 0 sees key 0 only: dequantized V up to p = 2^arg, |arg| <= 1.5 ct (see the single-key test)
+    q8, qs = orc.quant_q(q)
+    ct0 = float(orc.logit_scale_base(64)) * float(qs[0, 0, 0]) * float(ks[0, 0, 0])
+    assert np.abs(out[0, 0, 0] / deq0 - 1.0).max() <= np.exp2(1.51 * ct0) - 1.0 + 1e-6
     # each row only depends on keys <= its index: changing the last key (in its own 32-key block, so no K scale
     # of an earlier block moves) leaves every row of the first 32 unchanged
     k2 = k.copy()
@@ -234,7 +244,12 @@ def test_emulation_softmax_bookkeeping_gives_exact_lse():
         logit2 = s * cl[..., None].astype(np.float64) * ksr[:, :, None, :]
         mx = logit2.max(-1)
         exact = mx + np.log2(np.exp2(logit2 - mx[..., None]).sum(-1))
-        assert np.allclose(lse2, exact, rtol=0, atol=2e-5), bn
+        # every exponent argument is within 1.5 ct + 2^-24 |cl m| of S ct - cl m: nk = neg - fp32(1.5 * 2^23 * ct)
+        # rounds twice, each time by at most half an ulp of ~1.5 * 2^23 * ct; the logsumexp moves by at most that
+        ct_max = (cl[..., None].astype(np.float64) * ks[:, :, None, :]).max(-1)
+        bound = 1.51 * ct_max + 2.0 ** -23 * np.abs(cl * m) + 2e-5
+        assert (np.abs(lse2 - exact) <= bound).all(), bn
+        assert bound.max() < 5e-3
 
 
 def test_split_emulation_gives_exact_lse_and_matches_unsplit():
@@ -257,11 +272,13 @@ def test_split_emulation_gives_exact_lse_and_matches_unsplit():
     mx = logit2.max(-1)
     exact = mx + np.log2(np.exp2(logit2 - mx[..., None]).sum(-1))
     ref = orc.sdpa_reference(q, k, v)
+    ct_max = (cl[..., None].astype(np.float64) * ks[:, :, None, :]).max(-1)
     for chunks in (2, 3, 5):
         out, m, l = orc.attention(q8, qs, k8, ks, v8, vs, 300, block_n=64, out_dtype="f32", return_stats=True,
                                   kv_split=(chunks, rows))
         lse2 = cl.astype(np.float64) * m + np.log2(l.astype(np.float64))
-        assert np.allclose(lse2, exact, rtol=0, atol=2e-5), chunks
+        # the bound of the unsplit bookkeeping test (exponent arguments within 1.5 ct of exact)
+        assert (np.abs(lse2 - exact) <= 1.51 * ct_max + 2.0 ** -23 * np.abs(cl * m) + 2e-5).all(), chunks
         assert np.array_equal(out[~rows], base[~rows]) and np.array_equal(m[~rows], m0[~rows])
         # the split keeps small probabilities that an unsplit tile flushes in E4M3, so it is compared with float64
         # attention, not with the unsplit emulation
