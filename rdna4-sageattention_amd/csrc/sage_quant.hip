@@ -196,17 +196,18 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restric
     uint4 w = make_uint4(0, 0, 0, 0);
     if (row < S) w = *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss);
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    uint32_t e[8];
+    float y[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float lo = fminf(fmaxf(elem_lo<DT>(ws[i]) * cs[2 * i], -448.0f), 448.0f);
-      const float hi = fminf(fmaxf(elem_hi<DT>(ws[i]) * cs[2 * i + 1], -448.0f), 448.0f);
-      e[2 * i] = f32_to_e4m3(lo);
-      e[2 * i + 1] = f32_to_e4m3(hi);
+      y[2 * i] = fminf(fmaxf(elem_lo<DT>(ws[i]) * cs[2 * i], -448.0f), 448.0f);
+      y[2 * i + 1] = fminf(fmaxf(elem_hi<DT>(ws[i]) * cs[2 * i + 1], -448.0f), 448.0f);
     }
-    uint32_t* t = reinterpret_cast<uint32_t*>(vtile + rr * PITCH + c8 * 8);
-    t[0] = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
-    t[1] = e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24);
+    // hardware E4M3 conversion (round to nearest even, subnormals kept; inputs are within +-448)
+    int t0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    t0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], t0, true);
+    int t1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+    t1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], t1, true);
+    *reinterpret_cast<uint2*>(vtile + rr * PITCH + c8 * 8) = make_uint2((uint32_t)t0, (uint32_t)t1);
   }
   __syncthreads();
 

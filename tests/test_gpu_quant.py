@@ -95,3 +95,30 @@ def test_quant_edge_values(dev):
         assert np.array_equal(k8, ek8) and np.array_equal(bits(ks), bits(eks)), dt
         assert np.array_equal(bits(vs), bits(evs)), dt
         assert np.array_equal(v8t, orc.v8_to_device_layout(ev8)), dt
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_quant_v_e4m3_rounding_points(dev, dt):
+    """V values on every E4M3 code, every midpoint between neighbours (ties to even), one input ulp either side of
+    each midpoint, and the subnormal range, both signs.  Channels 0-63 have amax 448 (scale exactly 1, so the
+    conversion sees these values as they are); channels 64-127 are scaled by 0.37, so it sees arbitrary float32
+    neighbours of them.  The kernel's E4M3 bytes must equal the oracle's round-to-nearest-even."""
+    codes = orc.e4m3_to_f32(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = (codes[:-1] + codes[1:]) / 2
+    cand = np.concatenate([codes, mids, np.nextafter(mids, 0), np.nextafter(mids, 1e9),
+                           np.arange(1, 64) * 2.0 ** -12, [2.0 ** -10, 3 * 2.0 ** -11, 2.0 ** -11]])
+    col = torch.from_numpy(cand).float().to(dt)
+    col = torch.unique(torch.cat([col, -col]))
+    S = col.numel() + 1
+    v = torch.empty(1, 1, S, 128, dtype=torch.float32)
+    v[0, 0, 0] = 448.0
+    v[0, 0, 1:] = col.float()[:, None]
+    v[..., 64:] *= 0.37
+    v = v.to(dt)
+    k = _randn((1, 1, S, 128), dt, 77)
+    k8, ks, v8t, vs = run_quant_kv(k.to(dev), v.to(dev))
+    _, _, ev8, evs = orc.quant_kv(hnd_np(k), hnd_np(v), seq_pad=k8.shape[2])
+    assert np.array_equal(bits(vs), bits(evs))
+    ev8t = orc.v8_to_device_layout(ev8)
+    bad = np.argwhere(v8t != ev8t)
+    assert bad.size == 0, f"{len(bad)} E4M3 mismatches, first at {bad[:5]}"
