@@ -112,13 +112,16 @@ int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const flo
                   int Skv, int D, int causal, int out_dtype, float* lse, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
-/* Workspace bytes sage_forward needs for this shape on the current device. */
+/* Workspace bytes sage_forward needs for this shape on the current device (attention split state + per-chunk V
+   maxima).  No counterpart in the reference. */
 int sage_forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* workspace_bytes);
 
 /*
- * The whole path in one call: v_amax, quant_q, quant_kv, attention, on one stream.  Replaces the body of
- * src/rdna4_sage/_attention.py:97-140 below check_supported.  Intermediates are caller-owned buffers with the
- * layouts above.
+ * The whole path in one call, on one stream.  Replaces the body of src/rdna4_sage/_attention.py:97-140 below
+ * check_supported.  Intermediates are caller-owned buffers with the layouts above.  With a workspace of
+ * sage_forward_workspace bytes: one launch quantizes Q and takes per-chunk V maxima, one quantizes K and V, then the
+ * attention (and the merge of split tiles).  With workspace NULL: V maxima by atomics (fill + v_amax), quant_q,
+ * quant_kv, unsplit attention.  Both give the same intermediates bit for bit.
  */
 int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                  int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb, int64_t oss,

@@ -112,14 +112,14 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
     v8t = torch.empty((B, Hkv, D, skp), device=dev, dtype=torch.uint8)
     vs = torch.empty((B, Hkv, D), device=dev, dtype=torch.float32)
     out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
-    ws_bytes = _capi.attn_plan(dev.index if dev.index is not None else torch.cuda.current_device(),
-                               B, H, Sq, Skv, D, bool(is_causal))[2]
-    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8) if ws_bytes else None
+    ws_bytes = _capi.forward_workspace(dev.index if dev.index is not None else torch.cuda.current_device(),
+                                       B, H, Hkv, Sq, Skv, D, bool(is_causal))
+    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         _capi.call("sage_forward", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),
                    B, H, Hkv, Sq, Skv, D, dt, int(bool(is_causal)), qs_fold_factor(sm_scale, D),
                    _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(v8t), _ptr(vs),
-                   _ptr(ws) if ws is not None else None, ws_bytes, stream)
+                   _ptr(ws), ws_bytes, stream)
     return out
 
 

@@ -91,3 +91,12 @@ def attn_plan(device_index: int, B: int, H: int, Sq: int, Skv: int, D: int, caus
         call("sage_attn_plan", B, H, Sq, Skv, D, int(causal), ctypes.byref(n_full), ctypes.byref(chunks),
              ctypes.byref(ws))
     return n_full.value, chunks.value, ws.value
+
+
+@functools.lru_cache(maxsize=4096)
+def forward_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv: int, D: int, causal: bool) -> int:
+    """Workspace bytes of sage_forward for this shape on device `device_index`."""
+    ws = ctypes.c_int64()
+    with torch.cuda.device(device_index):
+        call("sage_forward_workspace", B, H, Hkv, Sq, Skv, D, int(causal), ctypes.byref(ws))
+    return ws.value

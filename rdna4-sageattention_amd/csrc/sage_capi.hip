@@ -1,4 +1,4 @@
-// C ABI glue: error reporting, queries and the one-call forward (v_amax -> quant_q -> quant_kv -> attention).
+// C ABI glue: error reporting, queries and the one-call forward (quantizers -> attention).
 #include <stdio.h>
 #include <string.h>
 
@@ -30,6 +30,19 @@ int quant_kv_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, 
 int attn_impl(const int8_t*, const float*, const int8_t*, const float*, const uint8_t*, const float*, void*, int64_t,
               int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*, int64_t, void*);
 int attn_plan_impl(int, int, int, int, int, int, int*, int*, int64_t*);
+int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D);
+int forward_quant_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, const void*,
+                       int64_t, int64_t, int64_t, int, int, int, int, int, int, int, float, int8_t*, float*, float*,
+                       int8_t*, float*, uint8_t*, float*, void*);
+
+// sage_forward's workspace: the attention plan's partial state, then (256-byte aligned) the per-chunk V maxima.
+static int forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* attn_bytes,
+                             int64_t* total) {
+  int rc = attn_plan_impl(B, H, Sq, Skv, D, causal, nullptr, nullptr, attn_bytes);
+  if (rc) return rc;
+  *total = (*attn_bytes + 255) / 256 * 256 + vamax_partial_bytes(B, Hkv, Skv, D);
+  return SAGE_OK;
+}
 
 }  // namespace sage
 
@@ -56,7 +69,8 @@ int sage_forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int ca
   sage::clear_error();
   SAGE_REQUIRE(workspace_bytes != nullptr, "sage_forward_workspace: workspace_bytes is NULL");
   SAGE_REQUIRE(Hkv > 0 && H % Hkv == 0, "sage_forward_workspace: heads %d not a multiple of kv heads %d", H, Hkv);
-  return sage::attn_plan_impl(B, H, Sq, Skv, D, causal, nullptr, nullptr, workspace_bytes);
+  int64_t attn = 0;
+  return sage::forward_workspace(B, H, Hkv, Sq, Skv, D, causal, &attn, workspace_bytes);
 }
 
 int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
@@ -70,20 +84,27 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
   SAGE_REQUIRE(H % Hkv == 0, "sage_forward: heads %d not a multiple of kv heads %d", H, Hkv);
   if (D != 64 && D != 128) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 128)", D);
   if (causal && Sq != Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len == kv_len");
-  if (workspace != nullptr) {
-    int64_t need = 0;
-    int rc0 = sage::attn_plan_impl(B, H, Sq, Skv, D, causal, nullptr, nullptr, &need);
-    if (rc0) return rc0;
-    SAGE_REQUIRE(workspace_bytes >= need, "sage_forward: workspace of %lld bytes, the plan needs %lld",
-                 (long long)workspace_bytes, (long long)need);
-  }
   int rc;
-  if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;
-  if ((rc = sage::quant_q_impl(q, qsb, qss, qsh, B, H, Sq, D, dtype, qs_mul, q8, qs, stream))) return rc;
-  if ((rc = sage::quant_kv_impl(k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, k8, ks, v8t, stream)))
+  if (workspace == nullptr) {
+    // no workspace: V maxima by atomics (four quantization launches) and every attention tile whole
+    if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;
+    if ((rc = sage::quant_q_impl(q, qsb, qss, qsh, B, H, Sq, D, dtype, qs_mul, q8, qs, stream))) return rc;
+    if ((rc = sage::quant_kv_impl(k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, k8, ks, v8t, stream)))
+      return rc;
+    return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype, nullptr,
+                           nullptr, 0, stream);
+  }
+  int64_t attn_bytes = 0, need = 0;
+  if ((rc = sage::forward_workspace(B, H, Hkv, Sq, Skv, D, causal, &attn_bytes, &need))) return rc;
+  SAGE_REQUIRE(workspace_bytes >= need, "sage_forward: workspace of %lld bytes, the plan needs %lld",
+               (long long)workspace_bytes, (long long)need);
+  SAGE_REQUIRE(((uintptr_t)workspace & 255u) == 0, "sage_forward: workspace must be 256-byte aligned");
+  float* vpart = reinterpret_cast<float*>(static_cast<char*>(workspace) + (attn_bytes + 255) / 256 * 256);
+  if ((rc = sage::forward_quant_impl(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype,
+                                     qs_mul, q8, qs, vpart, k8, ks, v8t, vs, stream)))
     return rc;
   return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype, nullptr,
-                         workspace, workspace_bytes, stream);
+                         attn_bytes ? workspace : nullptr, attn_bytes, stream);
 }
 
 }  // extern "C"

@@ -55,12 +55,12 @@ __device__ __forceinline__ void quantize_store_i8(const float (&x)[EPL], float s
 // quant_q: grid = (ceil(S / 64) * B * H), block = 256 (4 waves x 16 rows)
 // ------------------------------------------------------------------------------------------------------------------
 template <int D, int DT>
-__global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
-                                                      int64_t sh, int H, int S, int row_tiles, float qs_mul,
-                                                      int8_t* __restrict__ q8, float* __restrict__ qs) {
+__device__ __forceinline__ void quant_q_rows(const uint16_t* __restrict__ x, int64_t sb, int64_t ss, int64_t sh, int H,
+                                             int S, int row_tiles, float qs_mul, int8_t* __restrict__ q8,
+                                             float* __restrict__ qs, int block) {
   constexpr int EPL = D / QUAD;
-  const int tile = blockIdx.x % row_tiles;
-  const int bh = blockIdx.x / row_tiles;
+  const int tile = block % row_tiles;
+  const int bh = block / row_tiles;
   const int b = bh / H, h = bh % H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 3;
@@ -86,6 +86,13 @@ __global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict
   if (valid && j == 0) qs[(int64_t)bh * S + row] = (s / (float)D) * qs_mul;
 }
 
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
+                                                      int64_t sh, int H, int S, int row_tiles, float qs_mul,
+                                                      int8_t* __restrict__ q8, float* __restrict__ qs) {
+  quant_q_rows<D, DT>(x, sb, ss, sh, H, S, row_tiles, qs_mul, q8, qs, blockIdx.x);
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // fill / v_amax
 // ------------------------------------------------------------------------------------------------------------------
@@ -94,16 +101,18 @@ __global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ p, int64_
   if (i < n) p[i] = value;
 }
 
-// grid = (chunks * B * Hkv), block = 256; each block reduces `chunk_rows` rows of one (batch, kv head)
-template <int D, int DT>
-__global__ __launch_bounds__(256) void v_amax_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t ss,
-                                                     int64_t sh, int Hkv, int S, int chunks, int chunk_rows,
-                                                     float* __restrict__ vs) {
+// One block reduces `chunk_rows` rows of one (batch, kv head) to per-channel max |v|.  PARTIAL: store the chunk's
+// maxima to out[(bh * chunks + chunk) * D + d]; otherwise combine into out[bh * D + d] with atomicMax on the fp32 bit
+// pattern (values are >= 0, so unsigned order == float order; out must start at zero).
+template <int D, int DT, bool PARTIAL>
+__device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64_t sb, int64_t ss, int64_t sh,
+                                           int Hkv, int S, int chunks, int chunk_rows, float* __restrict__ out,
+                                           int block) {
   constexpr int LPR = D / 8;      // lanes per row, 8 elements (16 bytes) each
   constexpr int RPI = 256 / LPR;  // rows per iteration
   __shared__ float red[RPI][D + 1];
-  const int chunk = blockIdx.x % chunks;
-  const int bh = blockIdx.x / chunks;
+  const int chunk = block % chunks;
+  const int bh = block / chunks;
   const int b = bh / Hkv, h = bh % Hkv;
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
   const int row_end = min(S, (chunk + 1) * chunk_rows);
@@ -127,19 +136,50 @@ __global__ __launch_bounds__(256) void v_amax_kernel(const uint16_t* __restrict_
     float a = 0.0f;
 #pragma unroll 8
     for (int r = 0; r < RPI; ++r) a = fmaxf(a, red[r][threadIdx.x]);
-    atomicMax(reinterpret_cast<unsigned int*>(vs + (int64_t)bh * D + threadIdx.x), __float_as_uint(a));
+    if (PARTIAL)
+      out[((int64_t)bh * chunks + chunk) * D + threadIdx.x] = a;
+    else
+      atomicMax(reinterpret_cast<unsigned int*>(out + (int64_t)bh * D + threadIdx.x), __float_as_uint(a));
   }
+}
+
+// grid = (chunks * B * Hkv), block = 256
+template <int D, int DT>
+__global__ __launch_bounds__(256) void v_amax_kernel(const uint16_t* __restrict__ v, int64_t sb, int64_t ss,
+                                                     int64_t sh, int Hkv, int S, int chunks, int chunk_rows,
+                                                     float* __restrict__ vs) {
+  vamax_rows<D, DT, false>(v, sb, ss, sh, Hkv, S, chunks, chunk_rows, vs, blockIdx.x);
+}
+
+// The first pass of sage_forward in one launch: blocks [0, nv) write per-chunk V maxima (V_AMAX_ROWS rows each) to
+// `vpart`, blocks [nv, nv + q blocks) quantize Q.  The V blocks come first so their longer row loops start early.
+constexpr int V_AMAX_ROWS = 512;
+
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_q_vamax_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
+                                                            int64_t sh, int H, int Sq, int row_tiles, float qs_mul,
+                                                            int8_t* __restrict__ q8, float* __restrict__ qs,
+                                                            const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
+                                                            int64_t vsh, int Hkv, int Skv, int vchunks, int nv,
+                                                            float* __restrict__ vpart) {
+  if ((int)blockIdx.x < nv)
+    vamax_rows<D, DT, true>(v, vsb, vss, vsh, Hkv, Skv, vchunks, V_AMAX_ROWS, vpart, blockIdx.x);
+  else
+    quant_q_rows<D, DT>(x, sb, ss, sh, H, Sq, row_tiles, qs_mul, q8, qs, blockIdx.x - nv);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
 // quant_kv: grid = (Skp / 128 * B * Hkv), block = 256.  Wave w quantizes K rows [32w, 32w + 32) of the block (one K
 // scale) in two passes of 16 rows; then the block converts its 128 V rows to E4M3 and writes them transposed.
 // ------------------------------------------------------------------------------------------------------------------
+// vchunks == 0: vs holds the per-channel amax [B * Hkv][D].  vchunks > 0: vs holds per-chunk maxima
+// [B * Hkv][vchunks][D]; every block reduces them and block 0 of each (batch, kv head) stores the amax to vs_out.
 template <int D, int DT>
 __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss,
                                                        int64_t ksh, const uint16_t* __restrict__ v, int64_t vsb,
                                                        int64_t vss, int64_t vsh, int Hkv, int S, int Skp,
-                                                       const float* __restrict__ vs, int8_t* __restrict__ k8,
+                                                       const float* __restrict__ vs, int vchunks,
+                                                       float* __restrict__ vs_out, int8_t* __restrict__ k8,
                                                        float* __restrict__ ks, uint8_t* __restrict__ v8t) {
   constexpr int EPL = D / QUAD;
   constexpr int PITCH = D + 4;  // LDS row pitch of the [128 keys][D] E4M3 staging tile
@@ -186,9 +226,31 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restric
   constexpr int LPR = D / 8;      // lanes per row (8 channels each)
   constexpr int RPI = 256 / LPR;  // rows per pass
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
+  float am[8];
+  if (vchunks == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am[i] = vs[(int64_t)bh * D + c8 * 8 + i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am[i] = 0.0f;
+    for (int c = 0; c < vchunks; ++c) {
+      const v4f* p4 = reinterpret_cast<const v4f*>(vs + ((int64_t)bh * vchunks + c) * D + c8 * 8);
+      const v4f a = p4[0], b4 = p4[1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        am[i] = fmaxf(am[i], a[i]);
+        am[4 + i] = fmaxf(am[4 + i], b4[i]);
+      }
+    }
+    if (blk == 0 && r0 == 0) {
+      v4f* o4 = reinterpret_cast<v4f*>(vs_out + (int64_t)bh * D + c8 * 8);
+      o4[0] = v4f{am[0], am[1], am[2], am[3]};
+      o4[1] = v4f{am[4], am[5], am[6], am[7]};
+    }
+  }
   float cs[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) cs[i] = 448.0f / fmaxf(vs[(int64_t)bh * D + c8 * 8 + i], 1e-30f);
+  for (int i = 0; i < 8; ++i) cs[i] = 448.0f / fmaxf(am[i], 1e-30f);
   const uint16_t* vbase = v + b * vsb + h * vsh + c8 * 8;
 #pragma unroll 2
   for (int rr = r0; rr < 128; rr += RPI) {
@@ -289,7 +351,25 @@ static void launch_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh
   const int Skp = kv_pad(S);
   hipLaunchKernelGGL((quant_kv_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
                      static_cast<const uint16_t*>(k), ksb, kss, ksh, static_cast<const uint16_t*>(v), vsb, vss, vsh,
-                     Hkv, S, Skp, vs, k8, ks, v8t);
+                     Hkv, S, Skp, vs, 0, nullptr, k8, ks, v8t);
+}
+
+// sage_forward's quantization in two launches: Q + per-chunk V maxima, then K / V (reducing the maxima).
+template <int D, int DT>
+static void launch_forward_quant(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb,
+                                 int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, int B,
+                                 int H, int Hkv, int Sq, int Skv, float qs_mul, int8_t* q8, float* qs, float* vpart,
+                                 int8_t* k8, float* ks, uint8_t* v8t, float* vs, hipStream_t st) {
+  const int tiles = (Sq + 63) / 64;
+  const int vchunks = (Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS;
+  const int nv = vchunks * B * Hkv;
+  hipLaunchKernelGGL((quant_q_vamax_kernel<D, DT>), dim3(nv + tiles * B * H), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(q), qsb, qss, qsh, H, Sq, tiles, qs_mul, q8, qs,
+                     static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, vchunks, nv, vpart);
+  const int Skp = kv_pad(Skv);
+  hipLaunchKernelGGL((quant_kv_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(k), ksb, kss, ksh, static_cast<const uint16_t*>(v), vsb, vss, vsh,
+                     Hkv, Skv, Skp, vpart, vchunks, vs, k8, ks, v8t);
 }
 
 #define SAGE_DISPATCH_D_DT(D, DT, FN, ...)                                      \
@@ -336,6 +416,30 @@ int quant_kv_impl(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const vo
   SAGE_DISPATCH_D_DT(D, dtype, launch_quant_kv, k, ksb, kss, ksh, v, vsb, vss, vsh, B, Hkv, Skv, vs, k8, ks, v8t,
                      (hipStream_t)stream);
   return check_launch("quant_kv launch");
+}
+
+int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D) {
+  return (int64_t)B * Hkv * ((Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS) * D * (int64_t)sizeof(float);
+}
+
+// Validation of every argument is done by the caller (sage_forward) through the per-stage checks below.
+int forward_quant_impl(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
+                       int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, int B, int H, int Hkv, int Sq,
+                       int Skv, int D, int dtype, float qs_mul, int8_t* q8, float* qs, float* vpart, int8_t* k8,
+                       float* ks, uint8_t* v8t, float* vs, void* stream) {
+  const char* who = "sage_forward";
+  int rc = check_common(B, H, Sq, D, dtype, who);
+  if (rc) return rc;
+  if ((rc = check_common(B, Hkv, Skv, D, dtype, who))) return rc;
+  if ((rc = check_strided(q, qsb, qss, qsh, who, "q"))) return rc;
+  if ((rc = check_strided(k, ksb, kss, ksh, who, "k"))) return rc;
+  if ((rc = check_strided(v, vsb, vss, vsh, who, "v"))) return rc;
+  SAGE_REQUIRE(q8 && qs && vpart && k8 && ks && v8t && vs, "%s: an intermediate pointer is NULL", who);
+  SAGE_REQUIRE(aligned16(q8) && aligned16(k8) && aligned16(v8t) && aligned16(vpart) && aligned16(vs),
+               "%s: q8 / k8 / v8t / vs / workspace must be 16-byte aligned", who);
+  SAGE_DISPATCH_D_DT(D, dtype, launch_forward_quant, q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv,
+                     Sq, Skv, qs_mul, q8, qs, vpart, k8, ks, v8t, vs, (hipStream_t)stream);
+  return check_launch("quantization launch");
 }
 
 }  // namespace sage

@@ -3,6 +3,7 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_util import DT as DT_CODE
 from gpu_util import bits, hnd_np, run_quant_kv, run_quant_q
 from oracle import sage_oracle as orc
 
@@ -122,3 +123,45 @@ def test_quant_v_e4m3_rounding_points(dev, dt):
     ev8t = orc.v8_to_device_layout(ev8)
     bad = np.argwhere(v8t != ev8t)
     assert bad.size == 0, f"{len(bad)} E4M3 mismatches, first at {bad[:5]}"
+
+
+FWD_CASES = [  # B, H, Hkv, S, D, dtype
+    (1, 2, 2, 1000, 128, torch.bfloat16),
+    (2, 4, 2, 515, 64, torch.float16),
+    (1, 3, 1, 77, 128, torch.bfloat16),
+    (1, 24, 24, 4608, 128, torch.bfloat16),   # config 2 (Flux): 9 chunks of V maxima
+]
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,dt", FWD_CASES)
+@pytest.mark.parametrize("with_workspace", [True, False])
+def test_forward_intermediates_bitexact(dev, B, H, Hkv, S, D, dt, with_workspace):
+    """sage_forward's own intermediates: with a workspace the quantizers run fused (Q + per-chunk V maxima in one
+    launch, K / V reducing the maxima in the next), without one as four launches; both must equal the oracle."""
+    from cdna4_sage import _capi
+    q = _randn((B, H, S, D), dt, 3 + S).to(dev)
+    k = _randn((B, Hkv, S, D), dt, 4 + S).to(dev)
+    v = _randn((B, Hkv, S, D), dt, 5 + S, scale=3.0).to(dev)
+    skp = _capi.kv_pad(S)
+    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
+    qs = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    k8 = torch.empty(B, Hkv, skp, D, dtype=torch.int8, device=dev)
+    ks = torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev)
+    v8t = torch.empty(B, Hkv, D, skp, dtype=torch.uint8, device=dev)
+    vs = torch.full((B, Hkv, D), 7.0, dtype=torch.float32, device=dev)    # stale values must be overwritten
+    out = torch.empty(B, S, H, D, dtype=dt, device=dev)
+    wsb = _capi.forward_workspace(dev.index or 0, B, H, Hkv, S, S, D, False) if with_workspace else 0
+    ws = torch.full((max(wsb, 1),), 0xFF, dtype=torch.uint8, device=dev)
+    hnd = lambda t: (t.stride(0), t.stride(2), t.stride(1))  # noqa: E731
+    _capi.call("sage_forward", q.data_ptr(), *hnd(q), k.data_ptr(), *hnd(k), v.data_ptr(), *hnd(v), out.data_ptr(),
+               out.stride(0), out.stride(1), out.stride(2), B, H, Hkv, S, S, D, DT_CODE[dt], 0, 1.0, q8.data_ptr(),
+               qs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(), vs.data_ptr(),
+               ws.data_ptr() if with_workspace else None, wsb, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    eq8, eqs = orc.quant_q(hnd_np(q.cpu()))
+    ek8, eks, ev8, evs = orc.quant_kv(hnd_np(k.cpu()), hnd_np(v.cpu()), seq_pad=skp)
+    assert np.array_equal(q8.cpu().numpy(), eq8) and np.array_equal(bits(qs.cpu().numpy()), bits(eqs))
+    assert np.array_equal(bits(vs.cpu().numpy()), bits(evs)), "VS mismatch"
+    assert np.array_equal(k8.cpu().numpy(), ek8) and np.array_equal(bits(ks.cpu().numpy()), bits(eks))
+    assert np.array_equal(v8t.cpu().numpy(), orc.v8_to_device_layout(ev8)), "V8T mismatch"
+    assert torch.isfinite(out.float()).all()
