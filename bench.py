@@ -99,12 +99,13 @@ def cpu_baseline(cfg, target_s=15.0):
 
 
 def profiled_traffic(cfg_key):
-    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (config 2)."""
+    """HBM bytes per attention call (attention kernel + merge of split tiles) from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (config 2)."""
     f = ROOT / "profiles" / "flux_config2_hbm_traffic.md"
     if cfg_key != "2" or not f.exists():
         return None, None
     for line in f.read_text().splitlines():
-        if line.startswith("attn_kernel traffic_bytes_per_launch:"):
+        if line.startswith("attention traffic_bytes_per_call:"):
             return int(line.split(":")[1]), str(f.relative_to(ROOT))
     return None, None
 
@@ -117,6 +118,8 @@ def main():
     ap.add_argument("--config", default="2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--compare-unsplit", action="store_true",
+                    help="also time the attention with every query tile whole (no workspace)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -178,16 +181,17 @@ def main():
     dt = _capi.DTYPE_BF16 if q.dtype == torch.bfloat16 else _capi.DTYPE_F16
     L = _capi.lib()
 
-    def k_amax():
-        L.sage_v_amax(v.data_ptr(), *vs_, B, Hkv, S, D, dt, vs.data_ptr(), st)
+    # the C forward call exactly as the step makes it (two quantization launches, attention, merge of split tiles)
+    fws = _capi.forward_workspace(0, B, H, Hkv, S, S, D, cfg.causal)
+    fwbuf = torch.empty(max(fws, 1), dtype=torch.uint8, device=dev)
 
-    def k_q():
-        L.sage_quant_q(q.data_ptr(), *hs, B, H, S, D, dt, 1.0, q8.data_ptr(), qs.data_ptr(), st)
+    def k_forward():
+        L.sage_forward(q.data_ptr(), *hs, k.data_ptr(), *ks_, v.data_ptr(), *vs_, out.data_ptr(), out.stride(0),
+                       out.stride(1), out.stride(2), B, H, Hkv, S, S, D, dt, int(cfg.causal), 1.0, q8.data_ptr(),
+                       qs.data_ptr(), k8.data_ptr(), ks.data_ptr(), v8t.data_ptr(), vs.data_ptr(), fwbuf.data_ptr(),
+                       fws, st)
 
-    def k_kv():
-        L.sage_quant_kv(k.data_ptr(), *ks_, v.data_ptr(), *vs_, B, Hkv, S, D, dt, vs.data_ptr(), k8.data_ptr(),
-                        ks.data_ptr(), v8t.data_ptr(), st)
-
+    # the attention launch(es) alone, on the intermediates the forward call left
     n_full, chunks, ws_bytes = _capi.attn_plan(0, B, H, S, S, D, cfg.causal)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
@@ -197,17 +201,14 @@ def main():
                         int(cfg.causal), dt, None, ws.data_ptr() if split and ws_bytes else None,
                         ws_bytes if split else 0, st)
 
-    k_amax(); k_q(); k_kv(); k_attn(); k_attn(False)
+    k_forward()
     torch.cuda.synchronize()
     it = args.kernel_iters
-    t_amax = time_events(k_amax, it)
-    t_q = time_events(k_q, it)
-    t_kv = time_events(k_kv, it)
+    t_fwd = time_events(k_forward, it)
     t_attn = time_events(k_attn, it)
-    t_attn_whole = time_events(lambda: k_attn(False), it)
+    t_attn_whole = time_events(lambda: k_attn(False), it) if args.compare_unsplit else None
     attn_tflops = ops / (t_attn * 1e-3) / 1e12
-    q_bytes = cfg.quant_q_bytes()
-    kv_bytes = cfg.quant_kv_bytes(skp)
+    quant_bytes = cfg.quant_q_bytes() + cfg.quant_kv_bytes(skp)
 
     # ---- torch SDPA bf16 on the same GPU, same method as the step ----
     sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=cfg.causal)  # noqa: E731
@@ -246,16 +247,17 @@ def main():
                               "kv_chunks": chunks, "workspace_bytes": ws_bytes}},
         "detail": {
             "call_frac_of_peak": round(tops / MFMA_PEAK_TFLOPS, 4),
-            "kernel_ms": {"v_amax+fill": round(t_amax, 5), "quant_q": round(t_q, 5), "quant_kv": round(t_kv, 5),
-                          "attn": round(t_attn, 5), "attn_without_split": round(t_attn_whole, 5)},
-            "quant_q_GBps": round(q_bytes / (t_q * 1e-3) / 1e9, 1),
-            "quant_kv_GBps": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
+            "kernel_ms": {"forward_capi": round(t_fwd, 5), "attn": round(t_attn, 5),
+                          "quant (forward - attn)": round(t_fwd - t_attn, 5)},
+            "quant_GBps": round(quant_bytes / ((t_fwd - t_attn) * 1e-3) / 1e9, 1),
             "hbm_peak_GBps": HBM_PEAK_GBS,
             "sdpa_bf16_gpu_ms": round(ms_sdpa, 4),
             "speedup_vs_sdpa_bf16": round(ms_sdpa / ms, 3),
             "device": torch.cuda.get_device_name(dev),
         },
     }
+    if t_attn_whole is not None:
+        result["detail"]["kernel_ms"]["attn_without_split"] = round(t_attn_whole, 5)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(cfg)

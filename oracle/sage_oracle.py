@@ -229,9 +229,9 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
 
     ``kv_split = (chunks, rows)``, rows a bool array [B, H, Sq], emulates the gfx950 kernel's split tiles (no
     counterpart in the reference): for those rows the key tiles run as ``chunks`` contiguous ranges (range c =
-    tiles [c * n // chunks, (c + 1) * n // chunks)), each with its own online softmax from m = -inf, merged with
-    M = max m_c, w_c = exp2((m_c - M) * cl), L = sum w_c l_c, O = sum w_c O_c (float32, chunk order), then the
-    usual epilogue with L."""
+    tiles [c * n // chunks, (c + 1) * n // chunks)), each with its own online softmax from m = -inf, stored as
+    (m_c, l_c, fp16(O_c / l_c)) and merged with M = max m_c, W_c = exp2((m_c - M) * cl) * l_c, L = sum W_c,
+    O = sum W_c * fp16(O_c / l_c) (float32, chunk order), then the usual epilogue with L."""
     B, H, Sq, D = q8.shape
     Hkv = k8.shape[1]
     assert block_n % KV_BLOCK == 0 and H % Hkv == 0
@@ -250,9 +250,12 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
         ll = np.zeros_like(l)
         oo = np.zeros_like(o)
         for oc, mc, lc in parts:
-            w = np.exp2(((mc - mm).astype(F32) * cl).astype(F32)).astype(F32)
-            ll = (ll + (w * lc).astype(F32)).astype(F32)
-            oo = (oo + (w[..., None] * oc).astype(F32)).astype(F32)
+            # each chunk's O is stored normalised by its own l, in fp16 (round to nearest even)
+            rl = (F32(1.0) / lc).astype(F32)
+            pn = (oc * rl[..., None]).astype(F32).astype(np.float16).astype(F32)
+            w = (np.exp2(((mc - mm).astype(F32) * cl).astype(F32)).astype(F32) * lc).astype(F32)
+            ll = (ll + w).astype(F32)
+            oo = (oo + (w[..., None] * pn).astype(F32)).astype(F32)
         o = np.where(rows[..., None], oo, o)
         m = np.where(rows, mm, m)
         l = np.where(rows, ll, l)

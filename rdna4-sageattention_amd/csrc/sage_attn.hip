@@ -50,10 +50,10 @@ __device__ __forceinline__ void copy16_to_lds(const void* g, void* lds) {
 
 constexpr int ATT_MAX_CHUNKS = 16;
 
-// Workspace of a split launch (units = split tiles x chunks): O partials fp32 [units][128 rows][D] (unnormalised,
-// relative to the chunk's m), then (m, l) float2 [units][128 rows].
-__host__ __device__ constexpr int64_t ws_ml_offset(int64_t units, int D) { return units * ATT_BM * D; }
-__host__ __device__ constexpr int64_t ws_bytes(int64_t units, int D) { return units * ATT_BM * (D + 2) * 4; }
+// Workspace of a split launch (units = split tiles x chunks): each chunk's O normalised by its own l, as fp16
+// [units][128 rows][D] (|O / l| <= 448, the E4M3 range of V8), then (m, l) as float2 [units][128 rows].
+__host__ __device__ constexpr int64_t ws_ml_offset(int64_t units, int D) { return units * ATT_BM * D * 2; }
+__host__ __device__ constexpr int64_t ws_bytes(int64_t units, int D) { return units * ATT_BM * (2 * D + 8); }
 
 template <int D, bool CAUSAL, int OUT_DT>
 __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
@@ -276,15 +276,20 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   if (split) {
     // partial state of this key range (workspace layout at ws_ml_offset), merged by attn_merge_kernel
     const int q = wave * 32 + ln;
-    float* po = part + ((int64_t)unit * ATT_BM + q) * D;
+    const float rl = 1.0f / lt;
+    uint16_t* po = reinterpret_cast<uint16_t*>(part) + ((int64_t)unit * ATT_BM + q) * D;
 #pragma unroll
     for (int i = 0; i < NPV; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4*>(po + 32 * i + 8 * g + 4 * hf) =
-            make_float4(o[i][4 * g + 0], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]);
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t h0 = f32_to_f16_bits(o[i][4 * g + 0] * rl), h1 = f32_to_f16_bits(o[i][4 * g + 1] * rl);
+        const uint32_t h2 = f32_to_f16_bits(o[i][4 * g + 2] * rl), h3 = f32_to_f16_bits(o[i][4 * g + 3] * rl);
+        *reinterpret_cast<uint2*>(po + 32 * i + 8 * g + 4 * hf) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+      }
     const int64_t units = (int64_t)(total - n_full) * chunks;
-    if (hf == 0) reinterpret_cast<float2*>(part + ws_ml_offset(units, D))[(int64_t)unit * ATT_BM + q] = make_float2(m, lt);
+    if (hf == 0)
+      reinterpret_cast<float2*>(reinterpret_cast<uint8_t*>(part) + ws_ml_offset(units, D))[(int64_t)unit * ATT_BM + q] =
+          make_float2(m, lt);
     return;
   }
   const float inv = (1.0f / 448.0f) / lt;
@@ -314,9 +319,9 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
 // ------------------------------------------------------------------------------------------------------------------
 // Merge of split tiles: one thread per (split tile s, row r, 4-channel group c), consecutive threads on consecutive
 // groups of a row, so partial reads and output writes are contiguous; every partial load of a thread is issued before
-// the first is used.  With M = max_i m_i over the chunks, w_i = 2^((m_i - M) * cl), L = sum_i w_i l_i and
-// O = sum_i w_i O_i (float32, chunk order), the output is (O * ((1/448) / L)) * VS and lse = ln2 * (cl * M + log2 L),
-// the epilogue of an unsplit tile.  grid = n_split * 128 * (D / 4) / 256 blocks of 256 threads.
+// the first is used.  With M = max_i m_i over the chunks, W_i = 2^((m_i - M) * cl) * l_i, L = sum_i W_i and
+// O = sum_i W_i * fp16(O_i / l_i) (float32, chunk order), the output is (O * ((1/448) / L)) * VS and
+// lse = ln2 * (cl * M + log2 L), the epilogue of an unsplit tile.  grid = n_split * 128 * (D / 4) / 256 blocks of 256 threads.
 // ------------------------------------------------------------------------------------------------------------------
 template <int D, int OUT_DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qs,
@@ -336,15 +341,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   const int b = bh / H, h = bh % H;
   const int bhk = b * Hkv + h / (H / Hkv);
   const int64_t units = (int64_t)n_split * chunks, unit0 = (int64_t)s * chunks;
-  const float2* ml = reinterpret_cast<const float2*>(part + ws_ml_offset(units, D)) + unit0 * ATT_BM + q;
-  const float* po = part + (unit0 * ATT_BM + q) * D + 4 * cg;
+  const float2* ml =
+      reinterpret_cast<const float2*>(reinterpret_cast<const uint8_t*>(part) + ws_ml_offset(units, D)) + unit0 * ATT_BM + q;
+  const uint16_t* po = reinterpret_cast<const uint16_t*>(part) + (unit0 * ATT_BM + q) * D + 4 * cg;
   float2 e[ATT_MAX_CHUNKS];
-  float4 oi[ATT_MAX_CHUNKS];
+  uint2 oi[ATT_MAX_CHUNKS];
 #pragma unroll
   for (int i = 0; i < ATT_MAX_CHUNKS; ++i) {
     if (i < chunks) {
       e[i] = ml[i * ATT_BM];
-      oi[i] = *reinterpret_cast<const float4*>(po + (int64_t)i * ATT_BM * D);
+      oi[i] = *reinterpret_cast<const uint2*>(po + (int64_t)i * ATT_BM * D);
     }
   }
   const float cl = c0 * qs[(int64_t)bh * Sq + qrow];
@@ -357,12 +363,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 #pragma unroll
   for (int i = 0; i < ATT_MAX_CHUNKS; ++i) {
     if (i < chunks) {
-      const float w = __builtin_amdgcn_exp2f((e[i].x - M) * cl);
-      L = L + w * e[i].y;
-      acc.x = acc.x + w * oi[i].x;
-      acc.y = acc.y + w * oi[i].y;
-      acc.z = acc.z + w * oi[i].z;
-      acc.w = acc.w + w * oi[i].w;
+      const float w = __builtin_amdgcn_exp2f((e[i].x - M) * cl) * e[i].y;  // chunk weight times its l
+      L = L + w;
+      acc.x = acc.x + w * f16_lo(oi[i].x);
+      acc.y = acc.y + w * f16_hi(oi[i].x);
+      acc.z = acc.z + w * f16_lo(oi[i].y);
+      acc.w = acc.w + w * f16_hi(oi[i].y);
     }
   }
   const float inv = (1.0f / 448.0f) / L;

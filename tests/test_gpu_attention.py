@@ -100,8 +100,8 @@ def test_split_plan_and_unsplit_call(dev, B, H, Sq, Skv, D):
     every tile whole and must match the unsplit emulation, the default call the split one."""
     n_full, chunks, ws = _capi.attn_plan(dev.index or 0, B, H, Sq, Skv, D, False)
     n_split = B * H * ((Sq + 127) // 128)
-    # fp32 O partials and (m, l) per row of each chunk
-    assert n_full == 0 and chunks >= 2 and ws == n_split * chunks * 128 * (D + 2) * 4
+    # per row of each chunk: fp16 O / l (D values) and fp32 (m, l)
+    assert n_full == 0 and chunks >= 2 and ws == n_split * chunks * 128 * (2 * D + 8)
     q, k, v = _inputs(B, H, H, Sq, Skv, D, torch.bfloat16, "HND", seed=B + Sq)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     from gpu_util import run_quant_kv, run_quant_q
