@@ -151,46 +151,25 @@ __global__ __launch_bounds__(256) void v_amax_kernel(const uint16_t* __restrict_
   vamax_rows<D, DT, false>(v, sb, ss, sh, Hkv, S, chunks, chunk_rows, vs, blockIdx.x);
 }
 
-// The first pass of sage_forward in one launch: blocks [0, nv) write per-chunk V maxima (V_AMAX_ROWS rows each) to
-// `vpart`, blocks [nv, nv + q blocks) quantize Q.  The V blocks come first so their longer row loops start early.
-constexpr int V_AMAX_ROWS = 512;
-
-template <int D, int DT>
-__global__ __launch_bounds__(256) void quant_q_vamax_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
-                                                            int64_t sh, int H, int Sq, int row_tiles, float qs_mul,
-                                                            int8_t* __restrict__ q8, float* __restrict__ qs,
-                                                            const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
-                                                            int64_t vsh, int Hkv, int Skv, int vchunks, int nv,
-                                                            float* __restrict__ vpart) {
-  if ((int)blockIdx.x < nv)
-    vamax_rows<D, DT, true>(v, vsb, vss, vsh, Hkv, Skv, vchunks, V_AMAX_ROWS, vpart, blockIdx.x);
-  else
-    quant_q_rows<D, DT>(x, sb, ss, sh, H, Sq, row_tiles, qs_mul, q8, qs, blockIdx.x - nv);
-}
+constexpr int V_AMAX_ROWS = 512;  // keys per V-maxima chunk in sage_forward
 
 // ------------------------------------------------------------------------------------------------------------------
-// quant_kv: grid = (Skp / 128 * B * Hkv), block = 256.  Wave w quantizes K rows [32w, 32w + 32) of the block (one K
-// scale) in two passes of 16 rows; then the block converts its 128 V rows to E4M3 and writes them transposed.
+// K: Hadamard -> int8 with one scale per 32 keys.
+//  quant_k_rows128: 128 keys per block, wave w quantizes keys [32w, 32w + 32) in two passes of 16 rows.
+//  quant_k_rows64:  64 keys per block, wave w rotates keys [16w, 16w + 16) and the two waves of a 32-key group
+//                   combine their maxima through LDS (half the registers of the two-pass form).
 // ------------------------------------------------------------------------------------------------------------------
-// vchunks == 0: vs holds the per-channel amax [B * Hkv][D].  vchunks > 0: vs holds per-chunk maxima
-// [B * Hkv][vchunks][D]; every block reduces them and block 0 of each (batch, kv head) stores the amax to vs_out.
 template <int D, int DT>
-__global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss,
-                                                       int64_t ksh, const uint16_t* __restrict__ v, int64_t vsb,
-                                                       int64_t vss, int64_t vsh, int Hkv, int S, int Skp,
-                                                       const float* __restrict__ vs, int vchunks,
-                                                       float* __restrict__ vs_out, int8_t* __restrict__ k8,
-                                                       float* __restrict__ ks, uint8_t* __restrict__ v8t) {
+__device__ __forceinline__ void quant_k_rows128(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss, int64_t ksh,
+                                                int Hkv, int S, int Skp, int8_t* __restrict__ k8,
+                                                float* __restrict__ ks, int block) {
   constexpr int EPL = D / QUAD;
-  constexpr int PITCH = D + 4;  // LDS row pitch of the [128 keys][D] E4M3 staging tile
-  __shared__ uint8_t vtile[128 * PITCH];
   const int nblk = Skp / 128;
-  const int blk = blockIdx.x % nblk;
-  const int bh = blockIdx.x / nblk;
+  const int blk = block % nblk;
+  const int bh = block / nblk;
   const int b = bh / Hkv, h = bh % Hkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 3;
-
   // ---- K ----
   float xf[2][EPL];
   float amax = 0.0f;
@@ -222,6 +201,60 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restric
   }
   if (lane == 0) ks[(int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 4 + wave] = s;
 
+}
+
+template <int D, int DT>
+__device__ __forceinline__ void quant_k_rows64(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss, int64_t ksh,
+                                               int Hkv, int S, int Skp, int8_t* __restrict__ k8,
+                                               float* __restrict__ ks, int block) {
+  constexpr int EPL = D / QUAD;
+  __shared__ float wave_max[4];
+  const int nblk = Skp / 64;
+  const int blk = block % nblk;
+  const int bh = block / nblk;
+  const int b = bh / Hkv, h = bh % Hkv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 3;
+  const int row = blk * 64 + wave * 16 + (lane >> 2);
+  const bool valid = row < S;
+  const uint16_t* src = k + b * ksb + (int64_t)(valid ? row : 0) * kss + h * ksh + j * EPL;
+  double xd[EPL];
+  load_row_slice<EPL, DT>(src, valid, xd);
+  fwht_f64<EPL, QUAD>(xd, j);
+  float xf[EPL];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    xf[i] = (float)xd[i];
+    amax = fmaxf(amax, fabsf(xf[i]));
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if (lane == 0) wave_max[wave] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wave_max[wave & ~1], wave_max[wave | 1]), 1e-12f);
+  const float s = amax / 127.0f;
+  const float r = 1.0f / s;
+  int8_t* dst = k8 + ((int64_t)bh * Skp + row) * D + j * EPL;
+  quantize_store_i8<EPL>(xf, s, r, dst, true);
+  if (lane == 0 && (wave & 1) == 0) ks[(int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 2 + (wave >> 1)] = s;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// V: E4M3 with the per-channel scale 448 / max(VS, 1e-30), 128 keys per block, transposed through LDS into V8T.
+// vchunks == 0: vs holds the per-channel amax [B * Hkv][D].  vchunks > 0: vs holds per-chunk maxima
+// [B * Hkv][vchunks][D]; every block reduces them and block 0 of each (batch, kv head) stores the amax to vs_out.
+// ------------------------------------------------------------------------------------------------------------------
+template <int D, int DT>
+__device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss, int64_t vsh,
+                                             int Hkv, int S, int Skp, const float* __restrict__ vs, int vchunks,
+                                             float* __restrict__ vs_out, uint8_t* __restrict__ v8t, int block) {
+  constexpr int PITCH = D + 4;  // LDS row pitch of the [128 keys][D] E4M3 staging tile
+  __shared__ uint8_t vtile[128 * PITCH];
+  const int nblk = Skp / 128;
+  const int blk = block % nblk;
+  const int bh = block / nblk;
+  const int b = bh / Hkv, h = bh % Hkv;
   // ---- V: scale, E4M3, stage [key][d] in LDS ----
   constexpr int LPR = D / 8;      // lanes per row (8 channels each)
   constexpr int RPI = 256 / LPR;  // rows per pass
@@ -304,6 +337,47 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restric
   }
 }
 
+// sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (V_AMAX_ROWS keys each) to `vpart`,
+// blocks [nv, nv + nk) quantize 64 keys of K each, the rest quantize Q.  The V blocks come first so their longer row
+// loops start early.
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_qk_vamax_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
+                                                             int64_t sh, int H, int Sq, int row_tiles, float qs_mul,
+                                                             int8_t* __restrict__ q8, float* __restrict__ qs,
+                                                             const uint16_t* __restrict__ k, int64_t ksb, int64_t kss,
+                                                             int64_t ksh, int Skp, int nk, int8_t* __restrict__ k8,
+                                                             float* __restrict__ ks, const uint16_t* __restrict__ v,
+                                                             int64_t vsb, int64_t vss, int64_t vsh, int Hkv, int Skv,
+                                                             int vchunks, int nv, float* __restrict__ vpart) {
+  const int blk = blockIdx.x;
+  if (blk < nv)
+    vamax_rows<D, DT, true>(v, vsb, vss, vsh, Hkv, Skv, vchunks, V_AMAX_ROWS, vpart, blk);
+  else if (blk < nv + nk)
+    quant_k_rows64<D, DT>(k, ksb, kss, ksh, Hkv, Skv, Skp, k8, ks, blk - nv);
+  else
+    quant_q_rows<D, DT>(x, sb, ss, sh, H, Sq, row_tiles, qs_mul, q8, qs, blk - nv - nk);
+}
+
+// quant_kv (stage entry point): grid = (Skp / 128 * B * Hkv), block = 256; K then V of 128 keys
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss,
+                                                       int64_t ksh, const uint16_t* __restrict__ v, int64_t vsb,
+                                                       int64_t vss, int64_t vsh, int Hkv, int S, int Skp,
+                                                       const float* __restrict__ vs, int8_t* __restrict__ k8,
+                                                       float* __restrict__ ks, uint8_t* __restrict__ v8t) {
+  quant_k_rows128<D, DT>(k, ksb, kss, ksh, Hkv, S, Skp, k8, ks, blockIdx.x);
+  quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vs, 0, nullptr, v8t, blockIdx.x);
+}
+
+// sage_forward's second launch: V only, reducing the per-chunk maxima of the first
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
+                                                      int64_t vsh, int Hkv, int S, int Skp,
+                                                      const float* __restrict__ vpart, int vchunks,
+                                                      float* __restrict__ vs, uint8_t* __restrict__ v8t) {
+  quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vpart, vchunks, vs, v8t, blockIdx.x);
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------------------------------------------------
@@ -351,25 +425,26 @@ static void launch_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh
   const int Skp = kv_pad(S);
   hipLaunchKernelGGL((quant_kv_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
                      static_cast<const uint16_t*>(k), ksb, kss, ksh, static_cast<const uint16_t*>(v), vsb, vss, vsh,
-                     Hkv, S, Skp, vs, 0, nullptr, k8, ks, v8t);
+                     Hkv, S, Skp, vs, k8, ks, v8t);
 }
 
-// sage_forward's quantization in two launches: Q + per-chunk V maxima, then K / V (reducing the maxima).
+// sage_forward's quantization in two launches: Q, K and per-chunk V maxima, then V (reducing the maxima).
 template <int D, int DT>
 static void launch_forward_quant(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb,
                                  int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, int B,
                                  int H, int Hkv, int Sq, int Skv, float qs_mul, int8_t* q8, float* qs, float* vpart,
                                  int8_t* k8, float* ks, uint8_t* v8t, float* vs, hipStream_t st) {
   const int tiles = (Sq + 63) / 64;
+  const int Skp = kv_pad(Skv);
   const int vchunks = (Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS;
   const int nv = vchunks * B * Hkv;
-  hipLaunchKernelGGL((quant_q_vamax_kernel<D, DT>), dim3(nv + tiles * B * H), dim3(256), 0, st,
+  const int nk = Skp / 64 * B * Hkv;
+  hipLaunchKernelGGL((quant_qk_vamax_kernel<D, DT>), dim3(nv + nk + tiles * B * H), dim3(256), 0, st,
                      static_cast<const uint16_t*>(q), qsb, qss, qsh, H, Sq, tiles, qs_mul, q8, qs,
+                     static_cast<const uint16_t*>(k), ksb, kss, ksh, Skp, nk, k8, ks,
                      static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, vchunks, nv, vpart);
-  const int Skp = kv_pad(Skv);
-  hipLaunchKernelGGL((quant_kv_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
-                     static_cast<const uint16_t*>(k), ksb, kss, ksh, static_cast<const uint16_t*>(v), vsb, vss, vsh,
-                     Hkv, Skv, Skp, vpart, vchunks, vs, k8, ks, v8t);
+  hipLaunchKernelGGL((quant_v_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, Skp, vpart, vchunks, vs, v8t);
 }
 
 #define SAGE_DISPATCH_D_DT(D, DT, FN, ...)                                      \
