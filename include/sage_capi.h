@@ -112,6 +112,16 @@ int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const flo
                   int Skv, int D, int causal, int out_dtype, float* lse, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/*
+ * Row logsumexp of (Q K^T) * sm_scale over the keys (natural log), fp32 [B, H, Sq], computed from the bf16 / fp16
+ * inputs with 16-bit MFMAs and fp32 accumulation (the value `return_lse` returns).  sm_scale <= 0 means 1/sqrt(D).
+ * Causal masks are bottom-right aligned and need Sq <= Skv.  q / k addressed like sage_quant_q / sage_quant_kv.
+ * Replaces the fp32 torch matmul + logsumexp of src/sageattention/core.py:36-57 (`_lse`).
+ */
+int sage_lse_fwd(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
+                 int64_t ksh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float sm_scale,
+                 float* lse, void* stream);
+
 /* Workspace bytes sage_forward needs for this shape on the current device (attention split state + per-chunk V
    maxima).  No counterpart in the reference. */
 int sage_forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* workspace_bytes);

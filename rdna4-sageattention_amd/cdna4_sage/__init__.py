@@ -15,9 +15,9 @@ import torch
 from torch.nn.attention.bias import causal_lower_right
 
 from . import ops
-from ._attention import ARCHS, HEAD_DIMS, Unsupported, check_supported, device_arch
+from ._attention import ARCHS, HEAD_DIMS, Unsupported, check_supported, device_arch, lse
 
-__all__ = ["sageattn", "attention", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
+__all__ = ["sageattn", "attention", "lse", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
 __version__ = "0.1.0"
 
 # The C binding behind F.scaled_dot_product_attention.  Apps that replace F.scaled_dot_product_attention with

@@ -126,3 +126,36 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
 def _out_strides(out: torch.Tensor):
     # out is (B, Sq, H, D): (batch, seq, head) element strides
     return out.stride(0), out.stride(1), out.stride(2)
+
+
+def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
+    """Row logsumexp of Q K^T * scale (natural log) over the keys, fp32 [B, H, q_len], from the 16-bit inputs on the
+    gfx950 LSE kernel (the value `return_lse` returns; reference: src/sageattention/core.py:36-57).  Causal masks are
+    bottom-right aligned and need q_len <= kv_len.  Raises Unsupported when the kernel cannot run these inputs."""
+    if layout not in ("HND", "NHD"):
+        raise Unsupported(f"layout {layout!r}")
+    if not (q.is_cuda and k.device == q.device):
+        raise Unsupported("tensors must be on one ROCm GPU")
+    if q.dtype not in DTYPES or k.dtype != q.dtype or q.dim() != 4 or k.dim() != 4:
+        raise Unsupported("4D fp16 / bf16 q and k of one dtype required")
+    if device_arch(q.device) not in ARCHS:
+        raise Unsupported("not a CDNA4 GPU")
+    if layout == "HND":
+        B, H, Sq, D = q.shape
+        Hkv, Skv = k.shape[1], k.shape[2]
+    else:
+        B, Sq, H, D = q.shape
+        Skv, Hkv = k.shape[1], k.shape[2]
+    if D not in HEAD_DIMS or k.shape[-1] != D or k.shape[0] != B or Hkv == 0 or H % Hkv:
+        raise Unsupported("head_dim / head counts")
+    if Sq == 0 or Skv == 0 or max(q.numel(), k.numel()) > _I32_MAX:
+        raise Unsupported("empty or too large")
+    if is_causal and Sq > Skv:
+        raise Unsupported("causal LSE needs q_len <= kv_len")
+    q, sq_ = _bsh(q, layout)
+    k, sk_ = _bsh(k, layout)
+    out = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        _capi.call("sage_lse_fwd", _ptr(q), *sq_, _ptr(k), *sk_, B, H, Hkv, Sq, Skv, D, DTYPES[q.dtype],
+                   int(bool(is_causal)), float(sm_scale or 0.0), _ptr(out), torch.cuda.current_stream(q.device).cuda_stream)
+    return out

@@ -40,6 +40,7 @@ SIGNATURES = {
     "sage_attn_plan": ([_I, _I, _I, _I, _I, _I, _P, _P, _P], _I),
     "sage_attn_fwd": ([_P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _L, _P], _I),
     "sage_forward_workspace": ([_I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "sage_lse_fwd": ([_P, _L, _L, _L, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P], _I),
     "sage_forward": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
                       _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
 }

@@ -62,7 +62,9 @@ const char* sage_manifest_json(void) {
          "\"v_amax\": {\"rows_per_block\": 256, \"threads\": 256}, "
          "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": 3, \"max_kv_chunks\": 16, "
          "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
-         "\"variants\": [\"d64\", \"d128\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}}";
+         "\"variants\": [\"d64\", \"d128\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
+         "\"lse\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"mfma\": \"v_mfma_f32_32x32x16_{bf16,f16}\", "
+         "\"causal\": \"bottom-right, q_len <= kv_len\"}}";
 }
 
 int sage_forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* workspace_bytes) {

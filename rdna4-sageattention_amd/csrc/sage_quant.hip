@@ -120,13 +120,23 @@ __device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64
   float m[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) m[i] = 0.0f;
-  for (int row = chunk * chunk_rows + r0; row < row_end; row += RPI) {
-    const uint4 w = *reinterpret_cast<const uint4*>(base + (int64_t)row * ss);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  // eight rows per thread in flight: issue the loads of a group, then reduce them
+  constexpr int G = 8;
+  for (int row0 = chunk * chunk_rows + r0; row0 < row_end; row0 += G * RPI) {
+    uint4 w[G];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m[2 * i] = fmaxf(m[2 * i], fabsf(elem_lo<DT>(ws[i])));
-      m[2 * i + 1] = fmaxf(m[2 * i + 1], fabsf(elem_hi<DT>(ws[i])));
+    for (int g = 0; g < G; ++g) {
+      const int row = row0 + g * RPI;
+      w[g] = row < row_end ? *reinterpret_cast<const uint4*>(base + (int64_t)row * ss) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint32_t ws[4] = {w[g].x, w[g].y, w[g].z, w[g].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        m[2 * i] = fmaxf(m[2 * i], fabsf(elem_lo<DT>(ws[i])));
+        m[2 * i + 1] = fmaxf(m[2 * i + 1], fabsf(elem_hi<DT>(ws[i])));
+      }
     }
   }
 #pragma unroll
@@ -285,12 +295,17 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
 #pragma unroll
   for (int i = 0; i < 8; ++i) cs[i] = 448.0f / fmaxf(am[i], 1e-30f);
   const uint16_t* vbase = v + b * vsb + h * vsh + c8 * 8;
-#pragma unroll 2
-  for (int rr = r0; rr < 128; rr += RPI) {
-    const int row = blk * 128 + rr;
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (row < S) w = *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  // all of the thread's 128 / RPI rows in flight before the first conversion
+  uint4 wv[128 / RPI];
+#pragma unroll
+  for (int g = 0; g < 128 / RPI; ++g) {
+    const int row = blk * 128 + r0 + g * RPI;
+    wv[g] = row < S ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int g = 0; g < 128 / RPI; ++g) {
+    const int rr = r0 + g * RPI;
+    const uint32_t ws[4] = {wv[g].x, wv[g].y, wv[g].z, wv[g].w};
     float y[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -25,8 +25,14 @@ def _as_hnd(t: torch.Tensor, tensor_layout: str) -> torch.Tensor:
 
 def _lse(q, k, tensor_layout, is_causal, sm_scale):
     """Row logsumexp of Q K^T * scale over the keys, fp32 [B, H, q_len], on the unquantized inputs
-    (reference: src/sageattention/core.py:36-57).  Causal masks are bottom-right aligned.  The query heads that share
-    a kv head are processed together with one fp32 batched product per row chunk."""
+    (reference: src/sageattention/core.py:36-57).  Causal masks are bottom-right aligned.  On gfx950 the LSE kernel
+    computes it (16-bit products exact in fp32, fp32 accumulation); elsewhere, and for shapes the kernel does not take,
+    the query heads that share a kv head are processed together with one fp32 batched product per row chunk."""
+    _as_hnd(q, tensor_layout)  # layout check (ValueError, as the reference)
+    try:
+        return cdna4_sage.lse(q, k, tensor_layout, sm_scale, is_causal)
+    except cdna4_sage.Unsupported:
+        pass
     q, k = _as_hnd(q, tensor_layout), _as_hnd(k, tensor_layout)
     B, H, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]

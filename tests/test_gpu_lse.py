@@ -1,0 +1,72 @@
+"""gfx950 LSE kernel (the row logsumexp `return_lse` returns) vs float64 on the CPU oracle and vs the reference's own
+gate: atol 2e-3, rtol 1e-4 against fp32 torch (tests/test_sageattention.py:70 of the reference)."""
+import numpy as np
+import pytest
+import torch
+
+import cdna4_sage
+import sageattention
+from oracle import sage_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
+    (1, 2, 2, 300, 300, 128, torch.bfloat16, "HND", False),
+    (2, 4, 2, 515, 515, 64, torch.float16, "NHD", False),
+    (1, 4, 1, 257, 257, 64, torch.bfloat16, "HND", True),
+    (1, 2, 2, 130, 777, 128, torch.float16, "HND", True),    # bottom-right causal with q_len < kv_len
+    (3, 2, 2, 77, 1031, 128, torch.bfloat16, "NHD", False),
+    (1, 3, 3, 1, 64, 128, torch.bfloat16, "HND", False),
+]
+
+
+def _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, H, Sq, D, generator=g) * 1.5).to(dt)
+    k = torch.randn(B, Hkv, Skv, D, generator=g).to(dt)
+    if layout == "NHD":
+        return q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    return q, k
+
+
+def _hnd(t, layout):
+    return (t if layout == "HND" else t.transpose(1, 2)).float().numpy()
+
+
+@pytest.mark.parametrize("B,H,Hkv,Sq,Skv,D,dt,layout,causal", CASES)
+def test_lse_vs_float64(dev, B, H, Hkv, Sq, Skv, D, dt, layout, causal):
+    q, k = _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=Sq * 7 + Skv)
+    got = cdna4_sage.lse(q.to(dev), k.to(dev), layout, None, causal).cpu().numpy()
+    assert got.shape == (B, H, Sq) and got.dtype == np.float32
+    ref = orc.lse_reference(_hnd(q, layout), _hnd(k, layout), causal=causal)
+    # 16-bit products are exact in fp32; what remains is the fp32 accumulation order and exp2 / log2 (~1 ulp)
+    assert np.abs(got - ref).max() <= 1e-4 + 1e-6 * np.abs(ref).max()
+
+
+def test_lse_sm_scale_and_reference_gate(dev):
+    """Config 5a shape on a sample (one kv group of 4 query heads, full sequence), explicit sm_scale, causal; checked
+    at the reference's own tolerance against fp32 torch."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, 4, 8192, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, 1, 8192, 128, generator=g).to(torch.bfloat16).to(dev)
+    for causal in (False, True):
+        got = cdna4_sage.lse(q, k, "HND", 0.07, causal)
+        sc = torch.matmul(q.float(), k.float().repeat_interleave(4, 1).transpose(-1, -2).contiguous()) * 0.07
+        if causal:
+            sc.masked_fill_(torch.ones(8192, 8192, device=dev, dtype=torch.bool).triu(1), float("-inf"))
+        torch.testing.assert_close(got, torch.logsumexp(sc, -1), atol=2e-3, rtol=1e-4)
+
+
+def test_lse_unsupported_and_return_lse_uses_kernel(dev):
+    q = torch.randn(1, 2, 100, 96, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(cdna4_sage.Unsupported):
+        cdna4_sage.lse(q, q, "HND")
+    q = torch.randn(1, 2, 300, 128, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 200, 128, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(cdna4_sage.Unsupported):
+        cdna4_sage.lse(q, k, "HND", None, True)                 # causal with q_len > kv_len: torch path instead
+    v = torch.randn(1, 2, 2048, 128, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(1, 2, 2048, 128, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 2048, 128, device=dev, dtype=torch.bfloat16)
+    _, lse = sageattention.sageattn(q, k, v, is_causal=True, return_lse=True)
+    torch.testing.assert_close(lse, cdna4_sage.lse(q, k, "HND", None, True), atol=0, rtol=0)
