@@ -150,7 +150,7 @@ def main():
     torch.cuda.synchronize()
 
     def step():
-        return sageattention.sageattn(q, k, v, tensor_layout="HND", is_causal=cfg.causal)
+        return sageattention.sageattn(q, k, v, tensor_layout="HND", is_causal=cfg.causal, return_lse=cfg.return_lse)
 
     assert cdna4_sage._worth_it(q, k, "HND", cfg.causal), "config must route to the gfx950 kernel"
     for _ in range(args.warmup):
@@ -211,7 +211,7 @@ def main():
     quant_bytes = cfg.quant_q_bytes() + cfg.quant_kv_bytes(skp)
 
     # ---- torch SDPA bf16 on the same GPU, same method as the step ----
-    sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=cfg.causal)  # noqa: E731
+    sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=cfg.causal, enable_gqa=Hkv != H)  # noqa: E731
     for _ in range(args.warmup):
         sdpa()
     torch.cuda.synchronize()
@@ -258,6 +258,11 @@ def main():
     }
     if t_attn_whole is not None:
         result["detail"]["kernel_ms"]["attn_without_split"] = round(t_attn_whole, 5)
+    if cfg.return_lse:
+        # the LSE the step returns, timed alone (bf16 MFMA kernel; 2 flops per multiply-add of Q K^T)
+        t_lse = time_events(lambda: cdna4_sage.lse(q, k, "HND", None, cfg.causal), it)
+        result["detail"]["kernel_ms"]["lse"] = round(t_lse, 5)
+        result["detail"]["lse_bf16_TFLOPs"] = round(2 * B * H * cfg.pairs() * D / (t_lse * 1e-3) / 1e12, 1)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(cfg)
