@@ -101,7 +101,8 @@ int sage_attn_plan(int B, int H, int Sq, int Skv, int D, int causal, int* n_full
 
 /*
  * int8 QK^T / fp8 PV flash attention with the reference's online softmax (lazy rescale, threshold 8 in log2
- * units), causal (bottom-right aligned, requires Sq == Skv) and grouped-query heads (H % Hkv == 0).
+ * units), causal (bottom-right aligned: query i sees keys j <= i + Skv - Sq; requires Sq <= Skv) and grouped-query
+ * heads (H % Hkv == 0).
  * Replaces the attn launch of src/rdna4_sage/_attention.py:133-139 (kernarg "<4Q3i4x6Q2i", build_kernels.py:331).
  * out: out + b*osb + s*oss + h*osh (element strides, head_dim contiguous), dtype out_dtype.
  * lse: optional fp32 [B, H, Sq] (natural-log logsumexp of the quantized logits); pass NULL to skip.
@@ -138,6 +139,31 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
                  int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float qs_mul,
                  int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace,
                  int64_t workspace_bytes, void* stream);
+
+/*
+ * Packed variable-length batches: the padded key rows per kv head (*kv_rows, for the K8 / KS / V8T buffers of
+ * sage_forward_varlen) and the bytes of its table workspace, from the packed sizes alone.  Either output may be NULL.
+ */
+int sage_varlen_layout(int batch, int H, int Hkv, int total_q, int total_k, int* kv_rows, int64_t* workspace_bytes);
+
+/*
+ * Packed variable-length attention in one stream-ordered pass, without reading cu_seqlens back to the host.
+ * Replaces the host loop of src/sageattention/core.py:66-89 (sageattn_varlen: cu_seqlens .tolist(), one sageattn
+ * call per sequence).  q: [total_q] tokens of H heads at q + t*qss + h*qsh (D contiguous); k / v: [total_k] tokens
+ * of Hkv heads; out: [total_q] tokens of H heads, dtype = input dtype.  cu_seqlens_q / cu_seqlens_k: device int32
+ * [batch + 1]; sequence i is queries [cu_q[i], cu_q[i+1]) against keys [cu_k[i], cu_k[i+1]), quantized and attended
+ * exactly as a sage_forward call on that sequence alone (causal: bottom-right per sequence; query rows that see no
+ * key are written as 0).  Rows outside every sequence are not written.  Intermediates (caller-owned, R = *kv_rows
+ * of sage_varlen_layout): q8 int8 [H][total_q][D], qs fp32 [H][total_q], k8 int8 [Hkv][R][D], ks fp32
+ * [Hkv][R / 32], v8t E4M3 [Hkv][D][R], vs fp32 [batch][Hkv][D]; sequence i's keys sit at rows kp[i] (sum of the
+ * earlier sequences' lengths rounded up to 128).  workspace: sage_varlen_layout bytes, 256-byte aligned.  cu_seqlens
+ * that decrease or pass total_q / total_k leave the output unwritten and set the workspace's first int32 to 1.
+ */
+int sage_forward_varlen(const void* q, int64_t qss, int64_t qsh, const void* k, int64_t kss, int64_t ksh,
+                        const void* v, int64_t vss, int64_t vsh, void* out, int64_t oss, int64_t osh,
+                        const int* cu_seqlens_q, const int* cu_seqlens_k, int batch, int H, int Hkv, int total_q,
+                        int total_k, int D, int dtype, int causal, float qs_mul, int8_t* q8, float* qs, int8_t* k8,
+                        float* ks, uint8_t* v8t, float* vs, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

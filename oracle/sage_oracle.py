@@ -259,7 +259,8 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
         o = np.where(rows[..., None], oo, o)
         m = np.where(rows, mm, m)
         l = np.where(rows, ll, l)
-    inv = (F32(1.0 / 448.0) / l).astype(F32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(l > 0, (F32(1.0 / 448.0) / l).astype(F32), F32(0.0)).astype(F32)   # no visible key: 0
     out = ((o * inv[..., None]).astype(F32) * vs[:, hk][:, :, None, :].astype(F32)).astype(F32)
     out = round_output(out, out_dtype)
     if return_stats:
@@ -305,9 +306,13 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
         with np.errstate(invalid="ignore"):
             need = ((m_cand - m).astype(F32) * cl).astype(F32) > F32(threshold)
         m_new = np.where(need, m_cand, m).astype(F32)
+        # a row that has seen no key yet (causal with q_len > kv_len) keeps m = -inf and p = 0; the gfx950 kernel
+        # offsets such rows from 0 instead of -inf so that corr and the exponents stay free of NaN (no counterpart
+        # in the reference, which sends these calls to SDPA)
+        m_ref = np.where(m_new == -np.inf, F32(0.0), m_new).astype(F32)
         with np.errstate(invalid="ignore"):
-            corr = np.exp2(((m - m_new).astype(F32) * cl).astype(F32)).astype(F32)
-        neg = (F32(0.0) - (cl * m_new).astype(F32)).astype(F32)
+            corr = np.exp2(((m - m_ref).astype(F32) * cl).astype(F32)).astype(F32)
+        neg = (F32(0.0) - (cl * m_ref).astype(F32)).astype(F32)
         ct = (cl[..., None] * kst[:, :, None, :]).astype(F32)    # [B, H, Sq, nsub]
         # the gfx950 kernel reads S as F = 1.5 * 2^23 + S (exact, |S| < 2^21) and folds the offset into the
         # additive term: arg = fma(F, ct, nk), nk = neg - fp32(1.5 * 2^23 * ct).  F * ct + nk is exact in float64
@@ -350,6 +355,27 @@ def sage_forward(q, k, v, causal=False, sm_scale=None, block_n=32, out_dtype="bf
     q8, qs = quant_q(q, sm_scale)
     k8, ks, v8, vs = quant_kv(k, v)
     return attention(q8, qs, k8, ks, v8, vs, k.shape[2], causal=causal, block_n=block_n, out_dtype=out_dtype)
+
+
+def sage_forward_varlen(q, k, v, cu_q, cu_k, causal=False, sm_scale=None, block_n=64, out_dtype="bf16"):
+    """Packed variable-length forward (src/sageattention/core.py:80-88: one call per sequence, NHD slices).
+    q [total_q, H, D], k / v [total_k, Hkv, D] float32 arrays holding bf16 / fp16 values; cu_q / cu_k [batch + 1].
+    Each sequence is quantized and attended on its own (sage_forward on its slices, bottom-right causal).  A sequence
+    with queries but no keys gives 0 rows; rows outside every sequence are NaN (the gfx950 path leaves them
+    unwritten)."""
+    out = np.full(q.shape, np.nan, dtype=F32)
+    for i in range(len(cu_q) - 1):
+        q0, q1, k0, k1 = int(cu_q[i]), int(cu_q[i + 1]), int(cu_k[i]), int(cu_k[i + 1])
+        if q1 == q0:
+            continue
+        if k1 == k0:
+            out[q0:q1] = 0.0
+            continue
+        hnd = lambda t: np.ascontiguousarray(t.transpose(1, 0, 2))[None]   # noqa: E731  [1, H, S, D]
+        o = sage_forward(hnd(q[q0:q1]), hnd(k[k0:k1]), hnd(v[k0:k1]), causal=causal, sm_scale=sm_scale,
+                         block_n=block_n, out_dtype=out_dtype)
+        out[q0:q1] = o[0].transpose(1, 0, 2)
+    return out
 
 
 # ----------------------------------------------------------------------------------------------------------

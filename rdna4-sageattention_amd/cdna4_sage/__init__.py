@@ -7,7 +7,9 @@ libsage_capi.so and launched through its C ABI on torch's current stream.
     out = cdna4_sage.sageattn(q, k, v, tensor_layout="HND")   # drop-in for sageattention.sageattn
 
 Routing mirrors the reference's src/rdna4_sage/__init__.py:20-84: masks, small problems, unsupported shapes or GPUs
-and causal calls with q_len != kv_len go to torch's SDPA binding; everything else runs the gfx950 kernels.
+and causal calls with q_len > kv_len go to torch's SDPA binding; everything else runs the gfx950 kernels (causal
+calls with q_len < kv_len too, bottom-right aligned, where the reference uses SDPA).  attention_varlen runs packed
+variable-length batches in one pass.
 """
 import os
 
@@ -15,9 +17,9 @@ import torch
 from torch.nn.attention.bias import causal_lower_right
 
 from . import ops
-from ._attention import ARCHS, HEAD_DIMS, Unsupported, check_supported, device_arch, lse
+from ._attention import ARCHS, HEAD_DIMS, Unsupported, attention_varlen, check_supported, device_arch, lse
 
-__all__ = ["sageattn", "attention", "lse", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
+__all__ = ["sageattn", "attention", "attention_varlen", "lse", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
 __version__ = "0.1.0"
 
 # The C binding behind F.scaled_dot_product_attention.  Apps that replace F.scaled_dot_product_attention with
@@ -48,7 +50,7 @@ def is_available(device=None) -> bool:
 
 def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False):
     """Run the int8/fp8 kernel; raises Unsupported if it cannot.  Output in the input layout and dtype.
-    Causal attention needs q_len == kv_len."""
+    Causal attention is bottom-right aligned and needs q_len <= kv_len."""
     out = ops.attention(q, k, v, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
     return out.transpose(1, 2) if tensor_layout == "HND" else out
 
@@ -84,7 +86,7 @@ def _worth_it(q, k, tensor_layout, is_causal=False):
 
 def sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, attn_mask=None, return_lse=False, **kwargs):
     """Drop-in for sageattention.sageattn.  Uses the gfx950 kernel when it applies and pays off, torch SDPA otherwise
-    (masks, causal with q_len != kv_len, unsupported shapes or GPUs, small problems).  Causal attention is
+    (masks, causal with q_len > kv_len, unsupported shapes or GPUs, small problems).  Causal attention is
     bottom-right aligned as in SageAttention / FlashAttention.  Extra SageAttention kwargs are ignored."""
     if return_lse:
         raise NotImplementedError("cdna4_sage: return_lse is not supported here; use sageattention.sageattn")

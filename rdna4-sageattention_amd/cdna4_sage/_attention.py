@@ -72,8 +72,8 @@ def check_supported(q, k, v, layout, is_causal=False):
         raise Unsupported(f"heads {q.shape[h_ax]} not a multiple of kv heads {k.shape[h_ax]}")
     if max(q.numel(), k.numel()) > _I32_MAX or k.shape[s_ax] == 0 or q.shape[s_ax] == 0:
         raise Unsupported("tensor too large for 32-bit indexing or empty")
-    if is_causal and q.shape[s_ax] != k.shape[s_ax]:
-        raise Unsupported("causal attention needs q_len == kv_len")
+    if is_causal and q.shape[s_ax] > k.shape[s_ax]:
+        raise Unsupported("causal attention needs q_len <= kv_len (bottom-right aligned)")
 
 
 def qs_fold_factor(sm_scale, head_dim: int) -> float:
@@ -88,7 +88,7 @@ def _ptr(t: torch.Tensor) -> int:
 
 
 def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
-    """Attention without mask, optionally causal (q_len == kv_len).  q: (B, H, Sq, D) for "HND" or (B, Sq, H, D) for
+    """Attention without mask, optionally causal (bottom-right aligned, q_len <= kv_len).  q: (B, H, Sq, D) for "HND" or (B, Sq, H, D) for
     "NHD"; k/v alike, with H a multiple of the kv head count.  Returns (B, Sq, H, D) contiguous in q's dtype."""
     check_supported(q, k, v, layout, is_causal)
     dev = q.device
@@ -158,4 +158,61 @@ def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
     with torch.cuda.device(q.device):
         _capi.call("sage_lse_fwd", _ptr(q), *sq_, _ptr(k), *sk_, B, H, Hkv, Sq, Skv, D, DTYPES[q.dtype],
                    int(bool(is_causal)), float(sm_scale or 0.0), _ptr(out), torch.cuda.current_stream(q.device).cuda_stream)
+    return out
+
+
+def _packed(t: torch.Tensor):
+    """(token, head) element strides of a packed [tokens, heads, D] tensor, made contiguous when the kernels cannot
+    load it as 16-byte vectors."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or t.stride(0) % 8 or t.stride(1) % 8:
+        t = t.contiguous()
+    return t, (t.stride(0), t.stride(1))
+
+
+def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q=None, max_seqlen_k=None, sm_scale=None,
+                     is_causal=False):
+    """Packed variable-length attention in one stream-ordered pass (no host synchronisation): q [total_q, H, D],
+    k / v [total_k, Hkv, D], cu_seqlens_q / cu_seqlens_k [batch + 1] token offsets (int32 or int64, any device).
+    Sequence i is attention(q[cu_q[i]:cu_q[i+1]], k[cu_k[i]:cu_k[i+1]], v[...]) with its own quantization scales and
+    a bottom-right causal mask when is_causal; query rows of a causal sequence longer than its keys that see no key
+    are 0.  Rows outside every sequence are left unwritten (as torch.empty_like).  Returns [total_q, H, D].
+    The reference loops over the sequences on the host (src/sageattention/core.py:80-88).  Invalid cu_seqlens
+    (decreasing or past the totals) leave the output unwritten instead of raising, since they are not read back."""
+    if not (q.is_cuda and k.device == q.device and v.device == q.device):
+        raise Unsupported("tensors must be on one ROCm GPU")
+    if q.dtype not in DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise Unsupported(f"dtype {q.dtype}/{k.dtype}/{v.dtype} (fp16 or bf16 required)")
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
+        raise Unsupported("packed 3D q [total_q, H, D] and k / v [total_k, Hkv, D] of one shape required")
+    if device_arch(q.device) not in ARCHS:
+        raise Unsupported("not a CDNA4 GPU")
+    TQ, H, D = q.shape
+    TK, Hkv = k.shape[0], k.shape[1]
+    if D not in HEAD_DIMS or k.shape[-1] != D or Hkv == 0 or H % Hkv:
+        raise Unsupported(f"head_dim {D} / heads {H} / kv heads {Hkv}")
+    if cu_seqlens_q.dim() != 1 or cu_seqlens_q.shape != cu_seqlens_k.shape or cu_seqlens_q.numel() < 2:
+        raise Unsupported("cu_seqlens_q / cu_seqlens_k must be 1-D of one length batch + 1 >= 2")
+    if TQ == 0 or TK == 0 or max(q.numel(), k.numel()) > _I32_MAX:
+        raise Unsupported("empty or too large")
+    batch = cu_seqlens_q.numel() - 1
+    dev = q.device
+    cu_q = cu_seqlens_q.to(device=dev, dtype=torch.int32).contiguous()
+    cu_k = cu_seqlens_k.to(device=dev, dtype=torch.int32).contiguous()
+    q, sq_ = _packed(q)
+    k, sk_ = _packed(k)
+    v, sv_ = _packed(v)
+    tkp, ws_bytes = _capi.varlen_layout(batch, H, Hkv, TQ, TK)
+    q8 = torch.empty((H, TQ, D), device=dev, dtype=torch.int8)
+    qs = torch.empty((H, TQ), device=dev, dtype=torch.float32)
+    k8 = torch.empty((Hkv, tkp, D), device=dev, dtype=torch.int8)
+    ks = torch.empty((Hkv, tkp // KV_BLOCK), device=dev, dtype=torch.float32)
+    v8t = torch.empty((Hkv, D, tkp), device=dev, dtype=torch.uint8)
+    vs = torch.empty((batch, Hkv, D), device=dev, dtype=torch.float32)
+    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+    out = torch.empty((TQ, H, D), device=dev, dtype=q.dtype)
+    with torch.cuda.device(dev):
+        _capi.call("sage_forward_varlen", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), out.stride(0),
+                   out.stride(1), _ptr(cu_q), _ptr(cu_k), batch, H, Hkv, TQ, TK, D, DTYPES[q.dtype],
+                   int(bool(is_causal)), qs_fold_factor(sm_scale, D), _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks),
+                   _ptr(v8t), _ptr(vs), _ptr(ws), ws_bytes, torch.cuda.current_stream(dev).cuda_stream)
     return out

@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsage_capi.so"
 
 SAGE_OK, SAGE_ERR_INVALID, SAGE_ERR_UNSUPPORTED, SAGE_ERR_HIP = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F16 = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()
@@ -43,6 +43,9 @@ SIGNATURES = {
     "sage_lse_fwd": ([_P, _L, _L, _L, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P], _I),
     "sage_forward": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
                       _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
+    "sage_varlen_layout": ([_I, _I, _I, _I, _I, _P, _P], _I),
+    "sage_forward_varlen": ([_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _P,
+                             _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
 }
 
 
@@ -101,3 +104,12 @@ def forward_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv:
     with torch.cuda.device(device_index):
         call("sage_forward_workspace", B, H, Hkv, Sq, Skv, D, int(causal), ctypes.byref(ws))
     return ws.value
+
+
+@functools.lru_cache(maxsize=4096)
+def varlen_layout(batch: int, H: int, Hkv: int, total_q: int, total_k: int):
+    """(kv_rows, workspace_bytes) of sage_forward_varlen: padded packed key rows per kv head and the bytes of its
+    table workspace (host arithmetic only)."""
+    rows, ws = ctypes.c_int(), ctypes.c_int64()
+    call("sage_varlen_layout", batch, H, Hkv, total_q, total_k, ctypes.byref(rows), ctypes.byref(ws))
+    return rows.value, ws.value

@@ -55,12 +55,24 @@ constexpr int ATT_MAX_CHUNKS = 16;
 __host__ __device__ constexpr int64_t ws_ml_offset(int64_t units, int D) { return units * ATT_BM * D * 2; }
 __host__ __device__ constexpr int64_t ws_bytes(int64_t units, int D) { return units * ATT_BM * (2 * D + 8); }
 
-template <int D, bool CAUSAL, int OUT_DT>
+// Packed variable-length sequences (VARLEN): block i runs tile tiles[i] = (sequence, head, query tile) or exits when
+// its sequence is -1.  Q8 / QS rows are [H][TQ] (TQ = the `Sq` argument), K8 / KS / V8T the padded packed layout
+// of the quantizer (kv head stride / V8T channel stride `Skp` = TKP, sequence b from row kp[b]), VS [batch][Hkv][D],
+// output rows cu_q[b] + i with strides (oss, osh).
+struct VarlenTiles {
+  const int4* tiles;  // (sequence, head, query tile, 0) per block
+  const int* cu_q;    // [batch + 1]
+  const int* cu_k;    // [batch + 1]
+  const int* kp;      // [batch + 1] padded key offsets
+};
+
+template <int D, bool CAUSAL, int OUT_DT, bool VARLEN>
 __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ qs, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
-    int Sq, int Skv, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part, float c0) {
+    int Sq_arg, int Skv_arg, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part,
+    float c0, VarlenTiles vt) {
   constexpr int BN = ATT_BN;
   constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
   constexpr int VTILE = D * BN;      // bytes of the V tile  ([D channels][64 keys])
@@ -72,20 +84,44 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   constexpr int VLOADS = VTILE / 1024 / 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][TILE];
 
-  // ---- work decode: blocks [0, n_full) own whole query tiles (XCD-grouped); each later block owns one of the
-  // `chunks` key ranges of a split tile ----
-  const bool split = (int)blockIdx.x >= n_full;
-  int logical, unit = 0;
-  if (!split) {
-    logical = xcd_remap(blockIdx.x, n_full);
+  // ---- work decode.  Dense: blocks [0, n_full) own whole query tiles (XCD-grouped); each later block owns one of
+  // the `chunks` key ranges of a split tile.  VARLEN: the tile table. ----
+  const bool split = !VARLEN && (int)blockIdx.x >= n_full;
+  int b, h, qt, unit = 0, Sq = Sq_arg, Skv = Skv_arg;
+  int64_t qrow0;       // Q8 / QS row of query 0 of this (sequence, head)
+  int khead, kofs;     // K8 / KS / V8T head index and the sequence's first key row inside it
+  uint16_t* obase;
+  if (VARLEN) {
+    const int4 e = vt.tiles[blockIdx.x];
+    if (e.x < 0) return;
+    b = e.x;
+    h = e.y;
+    qt = e.z;
+    const int qb = vt.cu_q[b];
+    Sq = vt.cu_q[b + 1] - qb;
+    Skv = vt.cu_k[b + 1] - vt.cu_k[b];
+    qrow0 = (int64_t)h * Sq_arg + qb;
+    khead = h / (H / Hkv);
+    kofs = vt.kp[b];
+    obase = out + (int64_t)qb * oss;
   } else {
-    unit = blockIdx.x - n_full;
-    logical = n_full + unit / chunks;
+    int logical;
+    if (!split) {
+      logical = xcd_remap(blockIdx.x, n_full);
+    } else {
+      unit = blockIdx.x - n_full;
+      logical = n_full + unit / chunks;
+    }
+    const int bh = logical / q_tiles;
+    qt = logical % q_tiles;
+    if (CAUSAL) qt = q_tiles - 1 - qt;  // longest rows first within a head
+    b = bh / H;
+    h = bh % H;
+    qrow0 = (int64_t)bh * Sq;
+    khead = b * Hkv + h / (H / Hkv);
+    kofs = 0;
+    obase = out + b * osb;
   }
-  const int bh = logical / q_tiles;
-  int qt = logical % q_tiles;
-  if (CAUSAL) qt = q_tiles - 1 - qt;  // longest rows first within a head
-  const int b = bh / H, h = bh % H;
   const int hkv = h / (H / Hkv);
   const int bhk = b * Hkv + hkv;
 
@@ -101,15 +137,15 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   // ---- Q operand (B of the QK MFMA): lane (query ln, half hf) holds dims [32i + 16hf, +16) ----
   v4i qa[NQK];
   {
-    const int8_t* qp = q8 + ((int64_t)bh * Sq + qr) * D + 16 * hf;
+    const int8_t* qp = q8 + (qrow0 + qr) * D + 16 * hf;
 #pragma unroll
     for (int i = 0; i < NQK; ++i) qa[i] = *reinterpret_cast<const v4i*>(qp + 32 * i);
   }
-  const float cl = c0 * qs[(int64_t)bh * Sq + qr];
+  const float cl = c0 * qs[qrow0 + qr];
 
   // ---- KV range ----
   int kv_end = Skv;
-  if (CAUSAL) kv_end = min(Skv, qt * ATT_BM + ATT_BM + off);
+  if (CAUSAL) kv_end = max(0, min(Skv, qt * ATT_BM + ATT_BM + off));  // 0: no row of the tile sees a key
   const int ntiles = (kv_end + BN - 1) / BN;
   int t_lo = 0, t_hi = ntiles;
   if (split) {
@@ -118,9 +154,9 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     t_hi = (ch + 1) * ntiles / chunks;
   }
 
-  const int8_t* kbase = k8 + (int64_t)bhk * Skp * D;
-  const uint8_t* vbase = v8t + (int64_t)bhk * D * Skp;
-  const float* ksb = ks + (int64_t)bhk * (Skp / SAGE_KV_BLOCK);
+  const int8_t* kbase = k8 + ((int64_t)khead * Skp + kofs) * D;
+  const uint8_t* vbase = v8t + (int64_t)khead * D * Skp + kofs;
+  const float* ksb = ks + ((int64_t)khead * Skp + kofs) / SAGE_KV_BLOCK;
 
   // Source of each lane's direct loads.  Load j of wave w fills LDS chunk L = (w * LOADS + j) * 64 + lane of the
   // region, which must receive the tile chunk that the swizzled layout stores there.
@@ -190,11 +226,12 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] = __int_as_float(s_[kb_][v_]);        \
     if (MASKED) {                                                                                          \
-      const int kstart_ = t_ * BN;                                                                         \
+      /* element (kb, v) holds key t * 64 + 4 hf + c with the constant c = 32 kb + 8 (v / 4) + v % 4; it is    \
+         visible iff key <= min(Skv - 1, qr + off), i.e. c <= lim (one 32-bit bound per tile and lane) */   \
+      const int lim_ = (CAUSAL ? min(Skv - 1, qr + off) : Skv - 1) - (t_ * BN + 4 * hf);                   \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
-          const int key_ = kstart_ + 32 * kb_ + 8 * (v_ >> 2) + 4 * hf + (v_ & 3);                         \
-          if (key_ >= Skv || (CAUSAL && key_ > qr + off)) sf_[kb_][v_] = -INFINITY;                        \
+          if (32 * kb_ + 8 * (v_ >> 2) + (v_ & 3) > lim_) sf_[kb_][v_] = -INFINITY;                        \
         }                                                                                                  \
     }                                                                                                      \
     float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                              \
@@ -209,8 +246,11 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     const float mcand_ = fmaxf(m, rowmax_);                                                                \
     const bool need_ = (mcand_ - m) * cl > 8.0f;                                                           \
     const float mnew_ = need_ ? mcand_ : m;                                                                \
-    const float corr_ = __builtin_amdgcn_exp2f((m - mnew_) * cl);                                          \
-    const float neg_ = 0.0f - cl * mnew_;                                                                  \
+    /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets    \
+       from 0 instead of -inf keep corr and the exponents free of NaN */                                   \
+    const float mref_ = (MASKED && mnew_ == -INFINITY) ? 0.0f : mnew_;                                     \
+    const float corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                          \
+    const float neg_ = 0.0f - cl * mref_;                                                                  \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
     const float nk0_ = neg_ - SEED_F * ct0_, nk1_ = neg_ - SEED_F * ct1_;                                  \
     float psum_ = 0.0f;                                                                                    \
@@ -252,7 +292,7 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
   v16i seed16;
 #pragma unroll
   for (int v = 0; v < 16; ++v) seed16[v] = 0x4B400000;
-  SAGE_ISSUE_TILE(t_lo, t_lo & 1);
+  if (t_lo < t_hi) SAGE_ISSUE_TILE(t_lo, t_lo & 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   int t = t_lo;
@@ -292,9 +332,9 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
           make_float2(m, lt);
     return;
   }
-  const float inv = (1.0f / 448.0f) / lt;
+  const float inv = lt > 0.0f ? (1.0f / 448.0f) / lt : 0.0f;  // a row without any visible key is written as 0
   if (qvalid) {
-    uint16_t* orow = out + b * osb + (int64_t)qrow * oss + h * osh;
+    uint16_t* orow = obase + (int64_t)qrow * oss + h * osh;
     const float* vsr = vs + (int64_t)bhk * D;
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
@@ -309,9 +349,9 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
         *reinterpret_cast<uint2*>(orow + c) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
       }
     }
-    if (lse != nullptr && hf == 0) {
+    if (!VARLEN && lse != nullptr && hf == 0) {
       // sum_j exp(logit_ij) = 2^(cl * m) * l_total, so lse = ln2 * (cl * m + log2(l_total))
-      lse[(int64_t)bh * Sq + qrow] = 0.69314718055994531f * (cl * m + __log2f(lt));
+      lse[qrow0 + qrow] = 0.69314718055994531f * (cl * m + __log2f(lt));
     }
   }
 }
@@ -414,7 +454,7 @@ static int resident_blocks(int* per_cu) {
   static int cache = 0;
   if (cache == 0) {
     int n = 0;
-    SAGE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<D, CAUSAL, OUT_DT>, ATT_THREADS, 0),
+    SAGE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<D, CAUSAL, OUT_DT, false>, ATT_THREADS, 0),
                    "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     cache = n;
   }
@@ -469,9 +509,9 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
   const float c0 = (float)((1.0 / __builtin_sqrt((double)D)) * 1.4426950408889634);
   uint16_t* o = static_cast<uint16_t*>(out);
   float* part = static_cast<float*>(workspace);
-  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t, vs,
-                     o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks, part,
-                     c0);
+  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
+                     vs, o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks,
+                     part, c0, VarlenTiles{});
   if (n_split > 0) {
     if ((rc = check_launch("attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
@@ -484,7 +524,7 @@ static int check_attn_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int c
   SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "%s: sizes must be positive", who);
   SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
   if (D != 64 && D != 128) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 128)", who, D);
-  if (causal && Sq != Skv) return fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len == kv_len", who);
+  if (causal && Sq > Skv) return fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len <= kv_len", who);
   SAGE_REQUIRE((int64_t)B * H * ((Sq + ATT_BM - 1) / ATT_BM) * ATT_MAX_CHUNKS < (1ll << 31), "%s: too many query tiles",
                who);
   SAGE_REQUIRE((int64_t)D * kv_pad(Skv) < (1ll << 31), "%s: kv_len %d too long", who, Skv);
@@ -524,6 +564,31 @@ int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* 
                "%s: out strides must be non-negative multiples of 8 elements", who);
   return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn, q8, qs, k8, ks, v8t, vs, out, osb,
                             oss, osh, lse, B, H, Hkv, Sq, Skv, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+}  // namespace sage
+
+namespace sage {
+
+template <int D, bool CAUSAL, int OUT_DT>
+static int launch_attn_varlen(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks,
+                              const uint8_t* v8t, const float* vs, void* out, int64_t oss, int64_t osh, int H, int Hkv,
+                              int TQ, int TKP, int n_blocks, VarlenTiles vt, hipStream_t st) {
+  const float c0 = (float)((1.0 / __builtin_sqrt((double)D)) * 1.4426950408889634);
+  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
+                     v8t, vs, static_cast<uint16_t*>(out), (int64_t)0, oss, osh, nullptr, H, Hkv, TQ, 0, TKP, 0,
+                     n_blocks, n_blocks, 1, nullptr, c0, vt);
+  return check_launch("varlen attention launch");
+}
+
+// Validation is done by the caller (sage_forward_varlen).  n_blocks = entries of the tile table.
+int attn_varlen_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
+                     const float* vs, void* out, int64_t oss, int64_t osh, int H, int Hkv, int TQ, int TKP, int D,
+                     int causal, int out_dtype, int n_blocks, const void* tiles, const int* cu_q, const int* cu_k,
+                     const int* kp, void* stream) {
+  const VarlenTiles vt{static_cast<const int4*>(tiles), cu_q, cu_k, kp};
+  return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn_varlen, q8, qs, k8, ks, v8t, vs, out,
+                            oss, osh, H, Hkv, TQ, TKP, n_blocks, vt, (hipStream_t)stream);
 }
 
 }  // namespace sage

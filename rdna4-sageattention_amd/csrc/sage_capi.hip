@@ -48,7 +48,7 @@ static int forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int 
 
 extern "C" {
 
-int sage_abi_version(void) { return 2; }
+int sage_abi_version(void) { return 3; }
 
 const char* sage_last_error(void) { return sage::g_err; }
 
@@ -63,6 +63,7 @@ const char* sage_manifest_json(void) {
          "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": 3, \"max_kv_chunks\": 16, "
          "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
          "\"variants\": [\"d64\", \"d128\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
+         "\"varlen\": {\"meta_threads\": 1024, \"sort_bins\": 2048, \"kv_rows_per_sequence\": \"multiple of 128\"}, "
          "\"lse\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"mfma\": \"v_mfma_f32_32x32x16_{bf16,f16}\", "
          "\"causal\": \"bottom-right, q_len <= kv_len\"}}";
 }
@@ -85,7 +86,7 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
   SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "sage_forward: sizes must be positive");
   SAGE_REQUIRE(H % Hkv == 0, "sage_forward: heads %d not a multiple of kv heads %d", H, Hkv);
   if (D != 64 && D != 128) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 128)", D);
-  if (causal && Sq != Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len == kv_len");
+  if (causal && Sq > Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len <= kv_len");
   int rc;
   if (workspace == nullptr) {
     // no workspace: V maxima by atomics (four quantization launches) and every attention tile whole

@@ -101,33 +101,26 @@ __global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ p, int64_
   if (i < n) p[i] = value;
 }
 
-// One block reduces `chunk_rows` rows of one (batch, kv head) to per-channel max |v|.  PARTIAL: store the chunk's
-// maxima to out[(bh * chunks + chunk) * D + d]; otherwise combine into out[bh * D + d] with atomicMax on the fp32 bit
-// pattern (values are >= 0, so unsigned order == float order; out must start at zero).
-template <int D, int DT, bool PARTIAL>
-__device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64_t sb, int64_t ss, int64_t sh,
-                                           int Hkv, int S, int chunks, int chunk_rows, float* __restrict__ out,
-                                           int block) {
+// Per-channel max |v| over rows [row_beg, row_end) of one (batch, kv head): `base` points at channel 0 of row 0.
+// Returns the maximum of channel threadIdx.x in threads [0, D) (0 for an empty range).
+template <int D, int DT>
+__device__ __forceinline__ float vamax_core(const uint16_t* __restrict__ base, int64_t ss, int row_beg, int row_end) {
   constexpr int LPR = D / 8;      // lanes per row, 8 elements (16 bytes) each
   constexpr int RPI = 256 / LPR;  // rows per iteration
   __shared__ float red[RPI][D + 1];
-  const int chunk = block % chunks;
-  const int bh = block / chunks;
-  const int b = bh / Hkv, h = bh % Hkv;
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
-  const int row_end = min(S, (chunk + 1) * chunk_rows);
-  const uint16_t* base = v + b * sb + h * sh + c8 * 8;
+  const uint16_t* cb = base + c8 * 8;
   float m[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) m[i] = 0.0f;
   // eight rows per thread in flight: issue the loads of a group, then reduce them
   constexpr int G = 8;
-  for (int row0 = chunk * chunk_rows + r0; row0 < row_end; row0 += G * RPI) {
+  for (int row0 = row_beg + r0; row0 < row_end; row0 += G * RPI) {
     uint4 w[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int row = row0 + g * RPI;
-      w[g] = row < row_end ? *reinterpret_cast<const uint4*>(base + (int64_t)row * ss) : make_uint4(0, 0, 0, 0);
+      w[g] = row < row_end ? *reinterpret_cast<const uint4*>(cb + (int64_t)row * ss) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -142,10 +135,26 @@ __device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64
 #pragma unroll
   for (int i = 0; i < 8; ++i) red[r0][c8 * 8 + i] = m[i];
   __syncthreads();
+  float a = 0.0f;
   if (threadIdx.x < D) {
-    float a = 0.0f;
 #pragma unroll 8
     for (int r = 0; r < RPI; ++r) a = fmaxf(a, red[r][threadIdx.x]);
+  }
+  return a;
+}
+
+// One block reduces `chunk_rows` rows of one (batch, kv head) to per-channel max |v|.  PARTIAL: store the chunk's
+// maxima to out[(bh * chunks + chunk) * D + d]; otherwise combine into out[bh * D + d] with atomicMax on the fp32 bit
+// pattern (values are >= 0, so unsigned order == float order; out must start at zero).
+template <int D, int DT, bool PARTIAL>
+__device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64_t sb, int64_t ss, int64_t sh,
+                                           int Hkv, int S, int chunks, int chunk_rows, float* __restrict__ out,
+                                           int block) {
+  const int chunk = block % chunks;
+  const int bh = block / chunks;
+  const int b = bh / Hkv, h = bh % Hkv;
+  const float a = vamax_core<D, DT>(v + b * sb + h * sh, ss, chunk * chunk_rows, min(S, (chunk + 1) * chunk_rows));
+  if (threadIdx.x < D) {
     if (PARTIAL)
       out[((int64_t)bh * chunks + chunk) * D + threadIdx.x] = a;
     else
@@ -213,21 +222,19 @@ __device__ __forceinline__ void quant_k_rows128(const uint16_t* __restrict__ k, 
 
 }
 
+// 64 keys: local rows [local0, local0 + 64) of one (batch, kv head), `base` = row 0 of its source; rows >= nvalid
+// are zero.  Writes the 64 int8 rows at k8_blk and the two 32-key scales at ks_blk.
 template <int D, int DT>
-__device__ __forceinline__ void quant_k_rows64(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss, int64_t ksh,
-                                               int Hkv, int S, int Skp, int8_t* __restrict__ k8,
-                                               float* __restrict__ ks, int block) {
+__device__ __forceinline__ void quant_k64_core(const uint16_t* __restrict__ base, int64_t kss, int local0, int nvalid,
+                                               int8_t* __restrict__ k8_blk, float* __restrict__ ks_blk) {
   constexpr int EPL = D / QUAD;
   __shared__ float wave_max[4];
-  const int nblk = Skp / 64;
-  const int blk = block % nblk;
-  const int bh = block / nblk;
-  const int b = bh / Hkv, h = bh % Hkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 3;
-  const int row = blk * 64 + wave * 16 + (lane >> 2);
-  const bool valid = row < S;
-  const uint16_t* src = k + b * ksb + (int64_t)(valid ? row : 0) * kss + h * ksh + j * EPL;
+  const int r = wave * 16 + (lane >> 2);
+  const int row = local0 + r;
+  const bool valid = row < nvalid;
+  const uint16_t* src = base + (int64_t)(valid ? row : 0) * kss + j * EPL;
   double xd[EPL];
   load_row_slice<EPL, DT>(src, valid, xd);
   fwht_f64<EPL, QUAD>(xd, j);
@@ -244,27 +251,37 @@ __device__ __forceinline__ void quant_k_rows64(const uint16_t* __restrict__ k, i
   __syncthreads();
   amax = fmaxf(fmaxf(wave_max[wave & ~1], wave_max[wave | 1]), 1e-12f);
   const float s = amax / 127.0f;
-  const float r = 1.0f / s;
-  int8_t* dst = k8 + ((int64_t)bh * Skp + row) * D + j * EPL;
-  quantize_store_i8<EPL>(xf, s, r, dst, true);
-  if (lane == 0 && (wave & 1) == 0) ks[(int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 2 + (wave >> 1)] = s;
+  const float rs = 1.0f / s;
+  quantize_store_i8<EPL>(xf, s, rs, k8_blk + (int64_t)r * D + j * EPL, true);
+  if (lane == 0 && (wave & 1) == 0) ks_blk[wave >> 1] = s;
+}
+
+template <int D, int DT>
+__device__ __forceinline__ void quant_k_rows64(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss, int64_t ksh,
+                                               int Hkv, int S, int Skp, int8_t* __restrict__ k8,
+                                               float* __restrict__ ks, int block) {
+  const int nblk = Skp / 64;
+  const int blk = block % nblk;
+  const int bh = block / nblk;
+  const int b = bh / Hkv, h = bh % Hkv;
+  quant_k64_core<D, DT>(k + b * ksb + h * ksh, kss, blk * 64, S, k8 + ((int64_t)bh * Skp + blk * 64) * D,
+                        ks + (int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 2);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
 // V: E4M3 with the per-channel scale 448 / max(VS, 1e-30), 128 keys per block, transposed through LDS into V8T.
-// vchunks == 0: vs holds the per-channel amax [B * Hkv][D].  vchunks > 0: vs holds per-chunk maxima
-// [B * Hkv][vchunks][D]; every block reduces them and block 0 of each (batch, kv head) stores the amax to vs_out.
+// Core: local rows [local0, local0 + 128) of one (batch, kv head), `base` = row 0 of its source, rows >= nvalid are
+// zero.  vchunks == 0: `am_src` holds the (batch, kv head)'s per-channel amax [D].  vchunks > 0: `am_src` holds its
+// per-chunk maxima [vchunks][D]; they are reduced and, when vs_out is not NULL, the amax is stored there.  The 128
+// transposed keys go to v8t_blk + d * chan_stride (d = channel).
 // ------------------------------------------------------------------------------------------------------------------
 template <int D, int DT>
-__device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss, int64_t vsh,
-                                             int Hkv, int S, int Skp, const float* __restrict__ vs, int vchunks,
-                                             float* __restrict__ vs_out, uint8_t* __restrict__ v8t, int block) {
+__device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ base, int64_t vss, int local0, int nvalid,
+                                                const float* __restrict__ am_src, int vchunks,
+                                                float* __restrict__ vs_out, uint8_t* __restrict__ v8t_blk,
+                                                int64_t chan_stride) {
   constexpr int PITCH = D + 4;  // LDS row pitch of the [128 keys][D] E4M3 staging tile
   __shared__ uint8_t vtile[128 * PITCH];
-  const int nblk = Skp / 128;
-  const int blk = block % nblk;
-  const int bh = block / nblk;
-  const int b = bh / Hkv, h = bh % Hkv;
   // ---- V: scale, E4M3, stage [key][d] in LDS ----
   constexpr int LPR = D / 8;      // lanes per row (8 channels each)
   constexpr int RPI = 256 / LPR;  // rows per pass
@@ -272,12 +289,12 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
   float am[8];
   if (vchunks == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) am[i] = vs[(int64_t)bh * D + c8 * 8 + i];
+    for (int i = 0; i < 8; ++i) am[i] = am_src[c8 * 8 + i];
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) am[i] = 0.0f;
     for (int c = 0; c < vchunks; ++c) {
-      const v4f* p4 = reinterpret_cast<const v4f*>(vs + ((int64_t)bh * vchunks + c) * D + c8 * 8);
+      const v4f* p4 = reinterpret_cast<const v4f*>(am_src + (int64_t)c * D + c8 * 8);
       const v4f a = p4[0], b4 = p4[1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -285,8 +302,8 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
         am[4 + i] = fmaxf(am[4 + i], b4[i]);
       }
     }
-    if (blk == 0 && r0 == 0) {
-      v4f* o4 = reinterpret_cast<v4f*>(vs_out + (int64_t)bh * D + c8 * 8);
+    if (vs_out != nullptr && r0 == 0) {
+      v4f* o4 = reinterpret_cast<v4f*>(vs_out + c8 * 8);
       o4[0] = v4f{am[0], am[1], am[2], am[3]};
       o4[1] = v4f{am[4], am[5], am[6], am[7]};
     }
@@ -294,13 +311,13 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
   float cs[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) cs[i] = 448.0f / fmaxf(am[i], 1e-30f);
-  const uint16_t* vbase = v + b * vsb + h * vsh + c8 * 8;
+  const uint16_t* vbase = base + c8 * 8;
   // all of the thread's 128 / RPI rows in flight before the first conversion
   uint4 wv[128 / RPI];
 #pragma unroll
   for (int g = 0; g < 128 / RPI; ++g) {
-    const int row = blk * 128 + r0 + g * RPI;
-    wv[g] = row < S ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss) : make_uint4(0, 0, 0, 0);
+    const int row = local0 + r0 + g * RPI;
+    wv[g] = row < nvalid ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int g = 0; g < 128 / RPI; ++g) {
@@ -346,10 +363,25 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
                (((wd[i][2] >> (8 * ci)) & 0xFFu) << 16) | (((wd[i][3] >> (8 * ci)) & 0xFFu) << 24);
       }
       const int d = cg * 4 + ci;
-      uint8_t* dst = v8t + ((int64_t)bh * D + d) * Skp + blk * 128 + 64 * G + 16 * u;
+      uint8_t* dst = v8t_blk + (int64_t)d * chan_stride + 64 * G + 16 * u;
       *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
+}
+
+// dense layout: grid = (Skp / 128) * B * Hkv blocks; vs_out (vchunks > 0) is written by block 0 of each (b, kv head)
+template <int D, int DT>
+__device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss, int64_t vsh,
+                                             int Hkv, int S, int Skp, const float* __restrict__ vs, int vchunks,
+                                             float* __restrict__ vs_out, uint8_t* __restrict__ v8t, int block) {
+  const int nblk = Skp / 128;
+  const int blk = block % nblk;
+  const int bh = block / nblk;
+  const int b = bh / Hkv, h = bh % Hkv;
+  const float* am_src = vs + (int64_t)bh * (vchunks == 0 ? 1 : vchunks) * D;
+  float* out_row = (vchunks > 0 && blk == 0) ? vs_out + (int64_t)bh * D : nullptr;
+  quant_v128_core<D, DT>(v + b * vsb + h * vsh, vss, blk * 128, S, am_src, vchunks, out_row,
+                         v8t + (int64_t)bh * D * Skp + blk * 128, Skp);
 }
 
 // sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (V_AMAX_ROWS keys each) to `vpart`,
@@ -391,6 +423,66 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict
                                                       const float* __restrict__ vpart, int vchunks,
                                                       float* __restrict__ vs, uint8_t* __restrict__ v8t) {
   quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vpart, vchunks, vs, v8t, blockIdx.x);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Packed variable-length sequences.  Q is quantized as one sequence of TQ tokens ([H][TQ] rows: the per-token scale
+// does not depend on the sequence).  K8 / KS / V8T use a padded packed layout: sequence b's keys occupy rows
+// [kp[b], kp[b] + pad128(len_b)) of each kv head's TKP rows, so every 32-key scale block and every 64-key attention
+// tile lies inside one sequence, as in a separate call per sequence.  ktab[g] is the sequence that owns padded
+// 128-key block g (-1 past the last one).  vs [batch][Hkv][D] must be zero before the first launch.
+// ------------------------------------------------------------------------------------------------------------------
+struct VarlenKeys {
+  const int* cu_k;  // [batch + 1] token offsets of the sequences in k / v
+  const int* kp;    // [batch + 1] padded row offsets
+  const int* ktab;  // [TKP / 128] owner of each padded 128-key block
+};
+
+// first launch: blocks [0, nv) per-channel V maxima of one padded 128-key block (atomicMax into vs), [nv, nv + nk)
+// K of one padded 64-key block, the rest Q.  nv = Hkv * TKP / 128, nk = Hkv * TKP / 64.
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_varlen_kernel(const uint16_t* __restrict__ x, int64_t qss, int64_t qsh,
+                                                           int H, int TQ, int row_tiles, float qs_mul,
+                                                           int8_t* __restrict__ q8, float* __restrict__ qs,
+                                                           const uint16_t* __restrict__ k, int64_t kss, int64_t ksh,
+                                                           const uint16_t* __restrict__ v, int64_t vss, int64_t vsh,
+                                                           int Hkv, int TKP, VarlenKeys vk, int8_t* __restrict__ k8,
+                                                           float* __restrict__ ks, float* __restrict__ vs) {
+  const int nv = Hkv * (TKP / 128), nk = Hkv * (TKP / 64);
+  const int blk = blockIdx.x;
+  if (blk < nv) {
+    const int g = blk % (TKP / 128), h = blk / (TKP / 128);
+    const int seq = vk.ktab[g];
+    if (seq < 0) return;
+    const int kb = vk.cu_k[seq], n = vk.cu_k[seq + 1] - kb, local0 = g * 128 - vk.kp[seq];
+    if (local0 >= n) return;  // padding only
+    const float a = vamax_core<D, DT>(v + h * vsh + (int64_t)kb * vss, vss, local0, min(n, local0 + 128));
+    if (threadIdx.x < D)
+      atomicMax(reinterpret_cast<unsigned int*>(vs + ((int64_t)seq * Hkv + h) * D + threadIdx.x), __float_as_uint(a));
+  } else if (blk < nv + nk) {
+    const int i = blk - nv;
+    const int g = i % (TKP / 64), h = i / (TKP / 64);
+    const int seq = vk.ktab[g >> 1];
+    if (seq < 0) return;
+    const int kb = vk.cu_k[seq];
+    quant_k64_core<D, DT>(k + h * ksh + (int64_t)kb * kss, kss, g * 64 - vk.kp[seq], vk.cu_k[seq + 1] - kb,
+                          k8 + ((int64_t)h * TKP + g * 64) * D, ks + (int64_t)h * (TKP / SAGE_KV_BLOCK) + g * 2);
+  } else {
+    quant_q_rows<D, DT>(x, 0, qss, qsh, H, TQ, row_tiles, qs_mul, q8, qs, blk - nv - nk);
+  }
+}
+
+// second launch: V of one padded 128-key block per workgroup, grid = Hkv * TKP / 128
+template <int D, int DT>
+__global__ __launch_bounds__(256) void quant_v_varlen_kernel(const uint16_t* __restrict__ v, int64_t vss, int64_t vsh,
+                                                             int Hkv, int TKP, VarlenKeys vk,
+                                                             const float* __restrict__ vs, uint8_t* __restrict__ v8t) {
+  const int g = blockIdx.x % (TKP / 128), h = blockIdx.x / (TKP / 128);
+  const int seq = vk.ktab[g];
+  if (seq < 0) return;
+  const int kb = vk.cu_k[seq];
+  quant_v128_core<D, DT>(v + h * vsh + (int64_t)kb * vss, vss, g * 128 - vk.kp[seq], vk.cu_k[seq + 1] - kb,
+                         vs + ((int64_t)seq * Hkv + h) * D, 0, nullptr, v8t + (int64_t)h * D * TKP + g * 128, TKP);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -462,6 +554,21 @@ static void launch_forward_quant(const void* q, int64_t qsb, int64_t qss, int64_
                      static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, Skp, vpart, vchunks, vs, v8t);
 }
 
+template <int D, int DT>
+static void launch_varlen_quant(const void* q, int64_t qss, int64_t qsh, const void* k, int64_t kss, int64_t ksh,
+                                const void* v, int64_t vss, int64_t vsh, int H, int Hkv, int TQ, int TKP,
+                                float qs_mul, VarlenKeys vk, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                                uint8_t* v8t, float* vs, hipStream_t st) {
+  const int tiles = (TQ + 63) / 64;
+  const int nv = Hkv * (TKP / 128), nk = Hkv * (TKP / 64);
+  hipLaunchKernelGGL((quant_varlen_kernel<D, DT>), dim3(nv + nk + tiles * H), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(q), qss, qsh, H, TQ, tiles, qs_mul, q8, qs,
+                     static_cast<const uint16_t*>(k), kss, ksh, static_cast<const uint16_t*>(v), vss, vsh, Hkv, TKP,
+                     vk, k8, ks, vs);
+  hipLaunchKernelGGL((quant_v_varlen_kernel<D, DT>), dim3(nv), dim3(256), 0, st, static_cast<const uint16_t*>(v),
+                     vss, vsh, Hkv, TKP, vk, vs, v8t);
+}
+
 #define SAGE_DISPATCH_D_DT(D, DT, FN, ...)                                      \
   do {                                                                        \
     if ((D) == 64 && (DT) == SAGE_DTYPE_BF16) FN<64, DT_BF16>(__VA_ARGS__);    \
@@ -530,6 +637,17 @@ int forward_quant_impl(const void* q, int64_t qsb, int64_t qss, int64_t qsh, con
   SAGE_DISPATCH_D_DT(D, dtype, launch_forward_quant, q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv,
                      Sq, Skv, qs_mul, q8, qs, vpart, k8, ks, v8t, vs, (hipStream_t)stream);
   return check_launch("quantization launch");
+}
+
+// Validation is done by the caller (sage_forward_varlen); vs must already be zero.
+int varlen_quant_impl(const void* q, int64_t qss, int64_t qsh, const void* k, int64_t kss, int64_t ksh, const void* v,
+                      int64_t vss, int64_t vsh, int H, int Hkv, int TQ, int TKP, int D, int dtype, float qs_mul,
+                      const int* cu_k, const int* kp, const int* ktab, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                      uint8_t* v8t, float* vs, void* stream) {
+  const VarlenKeys vk{cu_k, kp, ktab};
+  SAGE_DISPATCH_D_DT(D, dtype, launch_varlen_quant, q, qss, qsh, k, kss, ksh, v, vss, vsh, H, Hkv, TQ, TKP, qs_mul, vk,
+                     q8, qs, k8, ks, v8t, vs, (hipStream_t)stream);
+  return check_launch("varlen quantization launch");
 }
 
 }  // namespace sage

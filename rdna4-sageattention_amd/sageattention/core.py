@@ -89,8 +89,21 @@ def sageattn_varlen(
     **kwargs: Any,
 ) -> torch.Tensor:
     """Packed variable-length attention: q [total_q, H, D], k / v [total_k, Hkv, D], cu_seqlens [batch + 1]
-    (reference: src/sageattention/core.py:79-102).  Each sequence is routed like a sageattn call; empty query
-    sequences are skipped."""
+    (reference: src/sageattention/core.py:66-89, a host loop of sageattn calls after reading cu_seqlens back).
+    On gfx950, when the longest key sequence reaches the kernel's minimum length (max_seqlen_k >= MIN_KV, or unknown),
+    the whole batch runs in one stream-ordered pass of the int8/fp8 kernels with per-sequence scales and no host
+    synchronisation; sequences that a per-sequence call would send to SDPA for being short are quantized there too.
+    Otherwise each sequence is routed like a sageattn call; empty query sequences are skipped."""
+    try:
+        mk = None if max_seqlen_k is None else int(max_seqlen_k)
+    except (TypeError, ValueError):
+        mk = None
+    if q.is_cuda and (mk is None or mk >= cdna4_sage.MIN_KV):
+        try:
+            return cdna4_sage.attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                               sm_scale=sm_scale, is_causal=is_causal)
+        except cdna4_sage.Unsupported:
+            pass
     bq = [int(x) for x in cu_seqlens_q.tolist()]
     bk = [int(x) for x in cu_seqlens_k.tolist()]
     out = torch.empty_like(q)

@@ -6,6 +6,7 @@ import json
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from cdna4_sage import _capi
@@ -75,7 +76,7 @@ def test_kv_and_attention_validation():
         return lib.sage_attn_fwd(*a.values())
 
     assert attn(H=3) == _capi.SAGE_ERR_INVALID and "multiple" in _err()
-    assert attn(causal=1, Skv=65) == _capi.SAGE_ERR_UNSUPPORTED and "q_len == kv_len" in _err()
+    assert attn(causal=1, Sq=65) == _capi.SAGE_ERR_UNSUPPORTED and "q_len <= kv_len" in _err()
     assert attn(D=256) == _capi.SAGE_ERR_UNSUPPORTED
     assert attn(out_dtype=3) == _capi.SAGE_ERR_UNSUPPORTED
     assert attn(q8=None) == _capi.SAGE_ERR_INVALID
@@ -84,7 +85,7 @@ def test_kv_and_attention_validation():
     n_full, chunks, ws = ctypes.c_int(-1), ctypes.c_int(-1), ctypes.c_int64(-1)
     refs = (ctypes.byref(n_full), ctypes.byref(chunks), ctypes.byref(ws))
     assert lib.sage_attn_plan(1, 4, 64, 64, 96, 0, *refs) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 96" in _err()
-    assert lib.sage_attn_plan(1, 4, 64, 65, 128, 1, *refs) == _capi.SAGE_ERR_UNSUPPORTED
+    assert lib.sage_attn_plan(1, 4, 65, 64, 128, 1, *refs) == _capi.SAGE_ERR_UNSUPPORTED
     assert lib.sage_attn_plan(0, 4, 64, 64, 128, 0, *refs) == _capi.SAGE_ERR_INVALID
     assert (n_full.value, chunks.value, ws.value) == (-1, -1, -1)       # outputs untouched on error
     wsb = ctypes.c_int64(-1)
@@ -94,9 +95,58 @@ def test_kv_and_attention_validation():
 
 def test_forward_validates_before_launching_and_python_raises():
     lib = _capi.lib()
-    rc = lib.sage_forward(P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128, 1, 4, 2, 64, 80, 128, 0, 1, 1.0,
+    rc = lib.sage_forward(P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128, 1, 4, 2, 80, 64, 128, 0, 1, 1.0,
                           P, P, P, P, P, P, None, 0, None)
     assert rc == _capi.SAGE_ERR_UNSUPPORTED and "causal" in _err()
     with pytest.raises(_capi.SageError, match="head_dim 80"):
         _capi.call("sage_quant_q", P, 0, 128, 0, 1, 1, 64, 80, 0, 1.0, P, P, None)
     assert isinstance(ctypes.CDLL, type)
+
+
+def test_varlen_layout_bounds():
+    """Padded key rows: sum of the sequences' lengths rounded up to 128 is at most total + 127 * batch; query tiles:
+    sum of ceil(len / 128) is at most (total + 127 * batch) / 128.  Tables are 256-byte aligned regions."""
+    lib = _capi.lib()
+    rows, ws = ctypes.c_int(-1), ctypes.c_int64(-1)
+    assert lib.sage_varlen_layout(3, 4, 2, 300, 500, ctypes.byref(rows), ctypes.byref(ws)) == _capi.SAGE_OK
+    assert rows.value == (500 + 127 * 3) // 128 * 128 == 768
+    # header, kp, order, tpre, ktab: one 256-byte region each; tiles: 4 heads x 5 query tiles x 16 bytes -> 512
+    assert ws.value == 5 * 256 + 512
+    assert _capi.varlen_layout(3, 4, 2, 300, 500) == (768, 1792)
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        batch = int(rng.integers(1, 40))
+        lk = rng.integers(0, 3000, batch)
+        lq = rng.integers(0, 3000, batch)
+        tk, tq = int(lk.sum()) + 1, int(lq.sum()) + 1
+        r, _ = _capi.varlen_layout(batch, 8, 2, tq, tk)
+        assert r % 128 == 0 and int(((lk + 127) // 128 * 128).sum()) <= r
+        tiles = int(((lq + 127) // 128).sum())
+        assert tiles <= (tq + 127 * batch) // 128
+    assert lib.sage_varlen_layout(0, 4, 2, 300, 500, None, None) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_varlen_layout(2, 4, 3, 300, 500, None, None) == _capi.SAGE_ERR_INVALID and "multiple" in _err()
+    assert lib.sage_varlen_layout(2, 4, 2, 300, 0, None, None) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_varlen_layout(1, 4, 2, 300, 2**24, None, None) == _capi.SAGE_ERR_INVALID and "too large" in _err()
+
+
+def test_varlen_validates_before_launching():
+    lib = _capi.lib()
+    _, ws_bytes = _capi.varlen_layout(2, 4, 2, 256, 256)
+    args = dict(q=P, qss=512, qsh=128, k=P, kss=256, ksh=128, v=P, vss=256, vsh=128, out=P, oss=512, osh=128,
+                cu_q=P, cu_k=P, batch=2, H=4, Hkv=2, total_q=256, total_k=256, D=128, dtype=0, causal=1, qs_mul=1.0,
+                q8=P, qs=P, k8=P, ks=P, v8t=P, vs=P, ws=P, ws_bytes=ws_bytes, stream=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.sage_forward_varlen(*a.values())
+
+    assert call(D=96) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 96" in _err()
+    assert call(dtype=2) == _capi.SAGE_ERR_UNSUPPORTED
+    assert call(Hkv=3) == _capi.SAGE_ERR_INVALID
+    assert call(q=P + 8) == _capi.SAGE_ERR_INVALID and "16-byte" in _err()
+    assert call(kss=100) == _capi.SAGE_ERR_INVALID and "multiples of 8" in _err()
+    assert call(cu_k=None) == _capi.SAGE_ERR_INVALID and "cu_seqlens" in _err()
+    assert call(v8t=None) == _capi.SAGE_ERR_INVALID
+    assert call(ws_bytes=ws_bytes - 1) == _capi.SAGE_ERR_INVALID and "workspace" in _err()
+    assert call(ws=P + 16) == _capi.SAGE_ERR_INVALID and "256-byte" in _err()
+    assert call(total_q=0) == _capi.SAGE_ERR_INVALID

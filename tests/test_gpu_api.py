@@ -107,11 +107,24 @@ def test_sm_scale_and_routing(dev):
     msk[..., :7] = float("-inf")
     torch.testing.assert_close(rdna4_sage.sageattn(qh, kh, vh, attn_mask=msk),
                                F.scaled_dot_product_attention(qh, kh, vh, attn_mask=msk))
-    # causal with q_len != kv_len -> SDPA with a bottom-right mask
+    # causal with q_len < kv_len below MIN_WORK -> SDPA with a bottom-right mask
     qs = qh[:, :, :1500]
     keep = torch.ones(1500, 2048, dtype=torch.bool, device=dev).tril(2048 - 1500)
     torch.testing.assert_close(rdna4_sage.sageattn(qs, kh, vh, is_causal=True),
                                F.scaled_dot_product_attention(qs, kh, vh, attn_mask=keep))
+
+
+def test_causal_q_shorter_than_kv_runs_the_kernel(dev):
+    """Bottom-right causal with q_len < kv_len above MIN_WORK: the kernel (the reference sends it to SDPA with
+    causal_lower_right), checked at the reference's gate against float32 attention with the same mask."""
+    g = torch.Generator().manual_seed(4)
+    q = rand((1, 24, 3000, 128), torch.bfloat16, g, dev)
+    k, v = (rand((1, 24, 4096, 128), torch.bfloat16, g, dev) for _ in range(2))
+    assert cdna4_sage._worth_it(q, k, "HND", True)
+    out = sageattention.sageattn(q, k, v, is_causal=True)
+    torch.testing.assert_close(out, cdna4_sage.attention(q, k, v, is_causal=True), rtol=0, atol=0)
+    heads = [0, 13]
+    assert cos(out[:, heads], ref_attention(q, k, v, causal=True, heads=heads)) > COS
 
 
 def test_routed_call_uses_the_kernel(dev):

@@ -27,6 +27,8 @@ CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 3, 3, 1024, 64, 128, torch.bfloat16, "NHD", False),
     (3, 2, 2, 77, 1031, 128, torch.bfloat16, "HND", False),
     (1, 8, 8, 1024, 1024, 64, torch.bfloat16, "HND", False),   # config 1 shape
+    (1, 2, 2, 130, 777, 128, torch.float16, "HND", True),      # bottom-right causal, q_len < kv_len
+    (2, 4, 2, 300, 1000, 64, torch.bfloat16, "NHD", True),
 ]
 
 

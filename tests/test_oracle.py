@@ -228,6 +228,52 @@ def test_emulation_causal_first_row_and_bottom_right():
     assert not np.array_equal(out[..., 39, :], out2[..., 39, :])
 
 
+def test_emulation_causal_q_longer_than_kv():
+    """Bottom-right causal with q_len > kv_len: row i sees keys <= i - (q_len - kv_len).  Rows that see no key are 0
+    (the gfx950 convention), and every other row equals the same query's row of the q_len == kv_len call on the last
+    kv_len queries, bit for bit (per-token Q scales and per-row softmax state do not depend on the other rows)."""
+    q, k, v = _bf16((1, 2, 70, 64), 40), _bf16((1, 2, 40, 64), 41), _bf16((1, 2, 40, 64), 42)
+    out = orc.sage_forward(q, k, v, causal=True, block_n=64, out_dtype="f32")
+    assert np.isfinite(out).all()
+    assert (out[:, :, :30] == 0).all()
+    tail = orc.sage_forward(np.ascontiguousarray(q[:, :, 30:]), k, v, causal=True, block_n=64, out_dtype="f32")
+    assert np.array_equal(out[:, :, 30:], tail)
+    ref = orc.sdpa_reference(q[:, :, 30:], k, v, causal=True)
+    assert _cos(out[:, :, 30:], ref) >= 0.999
+
+
+def test_emulation_causal_q_shorter_than_kv():
+    """q_len < kv_len: query i sees keys <= i + (kv_len - q_len), i.e. it is row i + kv_len - q_len of the square
+    causal call whose last q_len queries are these, bit for bit."""
+    q_all, k, v = _bf16((1, 2, 50, 64), 43), _bf16((1, 2, 50, 64), 44), _bf16((1, 2, 50, 64), 45)
+    q = np.ascontiguousarray(q_all[:, :, 30:])
+    out = orc.sage_forward(q, k, v, causal=True, block_n=64, out_dtype="f32")
+    full = orc.sage_forward(q_all, k, v, causal=True, block_n=64, out_dtype="f32")
+    assert np.array_equal(out, full[:, :, 30:])
+    assert not np.array_equal(out, orc.sage_forward(q, k, v, causal=False, block_n=64, out_dtype="f32"))
+
+
+def test_varlen_oracle_sequences_and_edge_rows():
+    """Packed batch with an empty query sequence, a sequence without keys and a causal sequence longer than its keys:
+    each sequence is its own call (pinned against float64 attention), rows outside every sequence stay NaN."""
+    H, Hkv, D = 4, 2, 64
+    cu_q = np.array([0, 37, 37, 100, 131, 160])
+    cu_k = np.array([0, 90, 150, 150, 170, 260])
+    q = _bf16((170, H, D), 46)       # rows 160.. belong to no sequence
+    k, v = _bf16((260, Hkv, D), 47), _bf16((260, Hkv, D), 48)
+    for causal in (False, True):
+        out = orc.sage_forward_varlen(q, k, v, cu_q, cu_k, causal=causal)
+        assert np.isnan(out[160:]).all() and np.isfinite(out[:160]).all()
+        assert (out[37:100] == 0).all()                              # sequence 2 has no keys
+        hnd = lambda t: np.ascontiguousarray(t.transpose(1, 0, 2))[None]   # noqa: E731
+        seqs = ((0, 37, 0, 90), (131, 160, 170, 260)) + (() if causal else ((100, 131, 150, 170),))
+        for (q0, q1, k0, k1) in seqs:
+            ref = orc.sdpa_reference(hnd(q[q0:q1]), hnd(k[k0:k1]), hnd(v[k0:k1]), causal=causal)[0].transpose(1, 0, 2)
+            assert _cos(out[q0:q1], ref) >= 0.999
+        if causal:   # sequence 3: 31 queries, 20 keys: the first 11 rows see no key
+            assert (out[100:111] == 0).all() and (out[111:131] != 0).any(axis=(1, 2)).all()
+
+
 def test_emulation_softmax_bookkeeping_gives_exact_lse():
     """The running max / lazy rescale / running sum must reproduce the logsumexp of the quantized logits
     S * QS * KS * sm computed directly; this fails for a dropped correction term or a misplaced K scale."""
