@@ -32,6 +32,11 @@ What each function restates (paths relative to the reference checkout):
                         fma(1.5 * 2^23 + S, ct, nk) form, which differs from the reference's S * ct - cl * m by
                         the rounding of nk (at most 1.5 * ct: S moved by less than 2 units, far below the int8
                         quantization error of S and the E4M3 step of p).
+                        Bottom-right causal for any q_len / kv_len: query i sees keys j <= i + kv_len - q_len; a
+                        query that sees no key (q_len > kv_len) gives a 0 row (the gfx950 convention; the reference
+                        sends such calls to SDPA, so this case has no reference value).
+* ``sage_forward_varlen`` src/sageattention/core.py:66-89 (`sageattn_varlen`): one ``sage_forward`` per sequence
+                        of the packed batch.
 * ``lse_reference``     src/sageattention/core.py:36-57 (`_lse`).
 
 All float32 steps are written as float32 numpy operations, which round to nearest even like the GPU's
