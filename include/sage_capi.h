@@ -14,17 +14,20 @@
  *  - Streams: `stream` is a hipStream_t (NULL = the default stream).
  *  - Element strides: (batch, seq, head) strides in elements; the head_dim axis must be contiguous; input base
  *    pointers 16-byte aligned and strides multiples of 8 elements (the quantizers load 16-byte vectors).
- *  - dtype: SAGE_DTYPE_BF16 or SAGE_DTYPE_F16; head_dim 64 or 128.
+ *  - dtype: SAGE_DTYPE_BF16 or SAGE_DTYPE_F16; head_dim D = 64, 96, 128 or 256 (kernel_build/build_kernels.py:26).
+ *    Q and K are rotated by the unnormalised Hadamard matrix of RB = min(D, 128) channels (block-diagonal for 256);
+ *    D = 96 is not rotated (kernel_build/build_kernels.py:36-37, sage_quant.py:18-30).
  *
- * Intermediate layouts (device memory, all contiguous):
- *  - Q8  int8  [B, H, Sq, D]              (head-major; the reference writes [B, Sq, H, D])
- *  - QS  fp32  [B, H, Sq]                 per-token scale / D, times the sm_scale fold factor
- *  - K8  int8  [B, Hkv, Skp, D]           Skp = sage_kv_pad(Skv); rows >= Skv are zero
- *  - KS  fp32  [B, Hkv, Skp / 32]         one scale per 32 keys (not divided by D)
- *  - V8T e4m3  [B, Hkv, D, Skp]           V * 448 / amax, transposed; inside every 64-key group key 8g + 4h + r is
+ * Intermediate layouts (device memory, all contiguous; DL = sage_layout_dim(D): D, or 128 for D = 96 whose rows are
+ * zero-padded so that the 128-channel attention kernel runs them):
+ *  - Q8  int8  [B, H, Sq, DL]             (head-major; the reference writes [B, Sq, H, D])
+ *  - QS  fp32  [B, H, Sq]                 per-token scale / RB (D = 96: the scale itself), times the sm_scale fold
+ *  - K8  int8  [B, Hkv, Skp, DL]          Skp = sage_kv_pad(Skv); rows >= Skv are zero
+ *  - KS  fp32  [B, Hkv, Skp / 32]         one scale per 32 keys (not divided by RB)
+ *  - V8T e4m3  [B, Hkv, DL, Skp]          V * 448 / amax, transposed; inside every 64-key group key 8g + 4h + r is
  *                                         stored at position 32h + 4g + r (the order the attention kernel's fp8 MFMA
  *                                         operand wants); keys >= Skv are zero
- *  - VS  fp32  [B, Hkv, D]                per-channel max |v| over the sequence
+ *  - VS  fp32  [B, Hkv, DL]               per-channel max |v| over the sequence (0 for padding channels)
  *
  * Workspace: sage_attn_fwd / sage_forward may split the key range of the query tiles of a short last round over
  * several workgroups (a plan that depends on the problem shape and the device's CU count, see sage_attn_plan); the
@@ -59,6 +62,10 @@ const char* sage_last_error(void);
 
 /* Padded KV length Skp used by K8 / KS / V8T. */
 int sage_kv_pad(int skv);
+
+/* Channels DL of the Q8 / K8 / V8T / VS layouts for head_dim D (D, or 128 for D = 96); 0 if D is not supported.
+   No counterpart in the reference (its Triton quantizers write D channels). */
+int sage_layout_dim(int head_dim);
 
 /* JSON description of the built kernels (architecture, head dims, tiles); static storage. */
 const char* sage_manifest_json(void);

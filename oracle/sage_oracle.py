@@ -109,6 +109,23 @@ def fwht_rows(x: np.ndarray) -> np.ndarray:
     return x
 
 
+def rotation_block(d: int) -> int:
+    """Channels of one Hadamard block for head_dim d: min(d, 128) for powers of two (kernel_build/build_kernels.py:27,
+    :36-37, HADAMARD_MAX = 128: block-diagonal for d = 256, sage_quant.py:18-30), 0 (no rotation) otherwise (d = 96)."""
+    return min(d, 128) if d & (d - 1) == 0 else 0
+
+
+def rotate_rows(x: np.ndarray) -> np.ndarray:
+    """The quantizers' rotation of the last axis (float64): one Sylvester Hadamard per block of rotation_block(d)
+    channels, or a plain float64 copy when d is not rotated."""
+    d = x.shape[-1]
+    rb = rotation_block(d)
+    if rb == 0:
+        return np.array(x, dtype=np.float64, copy=True)
+    lead = x.shape[:-1]
+    return fwht_rows(np.asarray(x).reshape(*lead, d // rb, rb)).reshape(*lead, d)
+
+
 # ----------------------------------------------------------------------------------------------------------
 # Rounding helpers
 # ----------------------------------------------------------------------------------------------------------
@@ -164,14 +181,16 @@ def quant_q(q: np.ndarray, sm_scale=None):
     """q: [B, H, S, D] float32 holding bf16/fp16 values (HND).
 
     Returns (q8 int8 [B, H, S, D], qs float32 [B, H, S]).  sage_quant.py:246-261; scale / RB because the
-    unnormalised Hadamard multiplies Q K^T by RB (:259-260); optional sm_scale fold (_attention.py:130-131)."""
+    unnormalised Hadamard multiplies Q K^T by RB (:259-260), the scale itself without rotation (d = 96); optional
+    sm_scale fold (_attention.py:130-131)."""
     d = q.shape[-1]
-    x = fwht_rows(q).astype(F32)
+    rb = rotation_block(d)
+    x = rotate_rows(q).astype(F32)
     a = np.maximum(np.abs(x).max(axis=-1), F32(1e-12)).astype(F32)
     s = (a / F32(127.0)).astype(F32)
     y = (x / s[..., None]).astype(F32)
     q8 = round_half_away_i8(y)
-    qs = (s / F32(d)).astype(F32)
+    qs = (s / F32(rb)).astype(F32) if rb else s
     f = qs_fold_factor(sm_scale, d)
     if f is not None:
         qs = (qs * f).astype(F32)
@@ -201,7 +220,7 @@ def quant_kv(k: np.ndarray, v: np.ndarray, vs: np.ndarray | None = None, seq_pad
         vs = v_amax(v)
     kp = np.zeros((B, Hkv, sp, D), dtype=F32)
     kp[:, :, :S] = k
-    x = fwht_rows(kp).astype(F32).reshape(B, Hkv, sp // KV_BLOCK, KV_BLOCK, D)
+    x = rotate_rows(kp).astype(F32).reshape(B, Hkv, sp // KV_BLOCK, KV_BLOCK, D)
     a = np.maximum(np.abs(x).max(axis=(-1, -2)), F32(1e-12)).astype(F32)
     ks = (a / F32(127.0)).astype(F32)
     y = (x / ks[..., None, None]).astype(F32)

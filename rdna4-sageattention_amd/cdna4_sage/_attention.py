@@ -18,6 +18,7 @@ _MANIFEST_PATH = Path(__file__).resolve().parent / "manifest.json"
 _MANIFEST = json.loads(_MANIFEST_PATH.read_text())
 KV_BLOCK = _MANIFEST["kv_block"]            # keys per K scale (reference: kernels/manifest.json "kv_block")
 HEAD_DIMS = tuple(_MANIFEST["head_dims"])
+LSE_HEAD_DIMS = tuple(_MANIFEST["lse"]["head_dims"])   # the LSE kernel; other head dims use the torch formula
 ARCHS = (_MANIFEST["arch"],)
 DTYPES = {torch.bfloat16: _capi.DTYPE_BF16, torch.float16: _capi.DTYPE_F16}
 _I32_MAX = 2**31 - 1
@@ -103,14 +104,15 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
     k, sk_ = _bsh(k, layout)
     v, sv_ = _bsh(v, layout)
     skp = _capi.kv_pad(Skv)
+    dl = _capi.layout_dim(D)    # head_dim 96 is stored zero-padded to 128 channels
     stream = torch.cuda.current_stream(dev).cuda_stream
 
-    q8 = torch.empty((B, H, Sq, D), device=dev, dtype=torch.int8)
+    q8 = torch.empty((B, H, Sq, dl), device=dev, dtype=torch.int8)
     qs = torch.empty((B, H, Sq), device=dev, dtype=torch.float32)
-    k8 = torch.empty((B, Hkv, skp, D), device=dev, dtype=torch.int8)
+    k8 = torch.empty((B, Hkv, skp, dl), device=dev, dtype=torch.int8)
     ks = torch.empty((B, Hkv, skp // KV_BLOCK), device=dev, dtype=torch.float32)
-    v8t = torch.empty((B, Hkv, D, skp), device=dev, dtype=torch.uint8)
-    vs = torch.empty((B, Hkv, D), device=dev, dtype=torch.float32)
+    v8t = torch.empty((B, Hkv, dl, skp), device=dev, dtype=torch.uint8)
+    vs = torch.empty((B, Hkv, dl), device=dev, dtype=torch.float32)
     out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
     ws_bytes = _capi.forward_workspace(dev.index if dev.index is not None else torch.cuda.current_device(),
                                        B, H, Hkv, Sq, Skv, D, bool(is_causal))
@@ -146,7 +148,7 @@ def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
     else:
         B, Sq, H, D = q.shape
         Skv, Hkv = k.shape[1], k.shape[2]
-    if D not in HEAD_DIMS or k.shape[-1] != D or k.shape[0] != B or Hkv == 0 or H % Hkv:
+    if D not in LSE_HEAD_DIMS or k.shape[-1] != D or k.shape[0] != B or Hkv == 0 or H % Hkv:
         raise Unsupported("head_dim / head counts")
     if Sq == 0 or Skv == 0 or max(q.numel(), k.numel()) > _I32_MAX:
         raise Unsupported("empty or too large")
@@ -202,12 +204,13 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q=None, max
     k, sk_ = _packed(k)
     v, sv_ = _packed(v)
     tkp, ws_bytes = _capi.varlen_layout(batch, H, Hkv, TQ, TK)
-    q8 = torch.empty((H, TQ, D), device=dev, dtype=torch.int8)
+    dl = _capi.layout_dim(D)
+    q8 = torch.empty((H, TQ, dl), device=dev, dtype=torch.int8)
     qs = torch.empty((H, TQ), device=dev, dtype=torch.float32)
-    k8 = torch.empty((Hkv, tkp, D), device=dev, dtype=torch.int8)
+    k8 = torch.empty((Hkv, tkp, dl), device=dev, dtype=torch.int8)
     ks = torch.empty((Hkv, tkp // KV_BLOCK), device=dev, dtype=torch.float32)
-    v8t = torch.empty((Hkv, D, tkp), device=dev, dtype=torch.uint8)
-    vs = torch.empty((batch, Hkv, D), device=dev, dtype=torch.float32)
+    v8t = torch.empty((Hkv, dl, tkp), device=dev, dtype=torch.uint8)
+    vs = torch.empty((batch, Hkv, dl), device=dev, dtype=torch.float32)
     ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
     out = torch.empty((TQ, H, D), device=dev, dtype=q.dtype)
     with torch.cuda.device(dev):

@@ -33,6 +33,7 @@ SIGNATURES = {
     "sage_abi_version": ([], _I),
     "sage_last_error": ([], ctypes.c_char_p),
     "sage_kv_pad": ([_I], _I),
+    "sage_layout_dim": ([_I], _I),
     "sage_manifest_json": ([], ctypes.c_char_p),
     "sage_quant_q": ([_P, _L, _L, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P], _I),
     "sage_v_amax": ([_P, _L, _L, _L, _I, _I, _I, _I, _I, _P, _P], _I),
@@ -85,6 +86,11 @@ def call(name: str, *args) -> None:
 
 def kv_pad(skv: int) -> int:
     return int(lib().sage_kv_pad(int(skv)))
+
+
+def layout_dim(head_dim: int) -> int:
+    """Channels of the Q8 / K8 / V8T / VS layouts for this head_dim (128 for 96, else head_dim)."""
+    return int(lib().sage_layout_dim(int(head_dim)))
 
 
 @functools.lru_cache(maxsize=4096)

@@ -35,11 +35,15 @@ constexpr int ATT_BM = 128;  // query rows per workgroup
 constexpr int ATT_BN = 64;   // keys per tile
 constexpr int ATT_THREADS = 256;
 
-// chunk swizzle for LDS rows of `row_bytes` (64 or 128)
+// chunk swizzle for LDS rows of `row_bytes` (64, 128 or 256)
 template <int ROW_BYTES> __device__ __forceinline__ int swz(int row, int chunk) {
+  if (ROW_BYTES == 256) return chunk ^ (row & 15);
   if (ROW_BYTES == 128) return chunk ^ ((row >> 1) & 7);
   return chunk ^ ((row >> 2) & 3);
 }
+
+// workgroups per CU the launch bounds ask for: d256 tiles take 64 KiB of LDS and twice the accumulators
+template <int D> constexpr int attn_occupancy() { return D == 256 ? 2 : 3; }
 
 // Direct global -> LDS copy of 16 bytes per lane: the data lands at LDS address (M0 base) + 16 * lane, so a wave
 // writes one contiguous KiB; `lds` must be wave-uniform.
@@ -66,13 +70,15 @@ struct VarlenTiles {
   const int* kp;      // [batch + 1] padded key offsets
 };
 
+// D is the channel count of the Q8 / K8 / V8T layouts; `dout` output channels are written (96 for head_dim 96, whose
+// layouts are zero-padded to 128; D otherwise).  c0 = log2(e) / sqrt(head_dim).
 template <int D, bool CAUSAL, int OUT_DT, bool VARLEN>
-__global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
+__global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ qs, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
     int Sq_arg, int Skv_arg, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part,
-    float c0, VarlenTiles vt) {
+    float c0, int dout, VarlenTiles vt) {
   constexpr int BN = ATT_BN;
   constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
   constexpr int VTILE = D * BN;      // bytes of the V tile  ([D channels][64 keys])
@@ -338,6 +344,7 @@ __global__ __launch_bounds__(ATT_THREADS, 3) void attn_kernel(
     const float* vsr = vs + (int64_t)bhk * D;
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
+      if (32 * i >= dout) break;  // head_dim 96: the zero-padded channels are not written
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c = 32 * i + 8 * g + 4 * hf;
@@ -368,10 +375,11 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
                                                          const float* __restrict__ vs, uint16_t* __restrict__ out,
                                                          int64_t osb, int64_t oss, int64_t osh,
                                                          float* __restrict__ lse, int H, int Hkv, int Sq, int q_tiles,
-                                                         int n_full, int n_split, int chunks, float c0) {
+                                                         int n_full, int n_split, int chunks, float c0, int dout) {
   constexpr int NG = D / 4;
   const int idx = blockIdx.x * 256 + threadIdx.x;
   const int cg = idx % NG;
+  if (4 * cg >= dout) return;  // head_dim 96: padding channels
   const int q = (idx / NG) % ATT_BM;
   const int s = idx / (NG * ATT_BM);
   const int logical = n_full + s;
@@ -486,10 +494,14 @@ static int make_plan(int B, int H, int Sq, int Skv, AttnPlan* p) {
   return SAGE_OK;
 }
 
+// c0 = log2(e) / sqrt(head_dim) with the kernel's built-in sm_scale (other scales are folded into QS)
+static float logit_scale_base(int head_dim) { return (float)((1.0 / __builtin_sqrt((double)head_dim)) * 1.4426950408889634); }
+
+// D: layout channels (64, 128 or 256); hd: head_dim (96 runs on the 128-channel layout)
 template <int D, bool CAUSAL, int OUT_DT>
 static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
                        const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, float* lse, int B, int H,
-                       int Hkv, int Sq, int Skv, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+                       int Hkv, int Sq, int Skv, int hd, void* workspace, int64_t workspace_bytes, hipStream_t st) {
   AttnPlan p;
   int rc;
   if (workspace == nullptr) {
@@ -506,16 +518,16 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
   const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
   const int n_split = p.n_tiles - p.n_full;
   const int blocks = p.n_full + n_split * p.chunks;
-  const float c0 = (float)((1.0 / __builtin_sqrt((double)D)) * 1.4426950408889634);
+  const float c0 = logit_scale_base(hd);
   uint16_t* o = static_cast<uint16_t*>(out);
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
                      vs, o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks,
-                     part, c0, VarlenTiles{});
+                     part, c0, hd, VarlenTiles{});
   if (n_split > 0) {
     if ((rc = check_launch("attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
-                       part, qs, vs, o, osb, oss, osh, lse, H, Hkv, Sq, q_tiles, p.n_full, n_split, p.chunks, c0);
+                       part, qs, vs, o, osb, oss, osh, lse, H, Hkv, Sq, q_tiles, p.n_full, n_split, p.chunks, c0, hd);
   }
   return check_launch("attention launch");
 }
@@ -523,19 +535,22 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
 static int check_attn_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, const char* who) {
   SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "%s: sizes must be positive", who);
   SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
-  if (D != 64 && D != 128) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 128)", who, D);
+  if (!head_dim_ok(D)) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 96, 128, 256)", who, D);
   if (causal && Sq > Skv) return fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len <= kv_len", who);
   SAGE_REQUIRE((int64_t)B * H * ((Sq + ATT_BM - 1) / ATT_BM) * ATT_MAX_CHUNKS < (1ll << 31), "%s: too many query tiles",
                who);
-  SAGE_REQUIRE((int64_t)D * kv_pad(Skv) < (1ll << 31), "%s: kv_len %d too long", who, Skv);
+  SAGE_REQUIRE((int64_t)layout_dim(D) * kv_pad(Skv) < (1ll << 31), "%s: kv_len %d too long", who, Skv);
   return SAGE_OK;
 }
 
-#define SAGE_ATTN_DISPATCH(D, CAUSAL, BF, FN, ...)                               \
-  ((D) == 128 ? ((CAUSAL) ? ((BF) ? FN<128, true, DT_BF16>(__VA_ARGS__) : FN<128, true, DT_F16>(__VA_ARGS__))  \
-                          : ((BF) ? FN<128, false, DT_BF16>(__VA_ARGS__) : FN<128, false, DT_F16>(__VA_ARGS__))) \
-              : ((CAUSAL) ? ((BF) ? FN<64, true, DT_BF16>(__VA_ARGS__) : FN<64, true, DT_F16>(__VA_ARGS__))    \
-                          : ((BF) ? FN<64, false, DT_BF16>(__VA_ARGS__) : FN<64, false, DT_F16>(__VA_ARGS__))))
+// dispatch on the layout channels (head_dim 96 -> 128)
+#define SAGE_ATTN_DISPATCH_DL(DL, CAUSAL, BF, FN, ...)                                                          \
+  ((CAUSAL) ? ((BF) ? FN<DL, true, DT_BF16>(__VA_ARGS__) : FN<DL, true, DT_F16>(__VA_ARGS__))                  \
+            : ((BF) ? FN<DL, false, DT_BF16>(__VA_ARGS__) : FN<DL, false, DT_F16>(__VA_ARGS__)))
+#define SAGE_ATTN_DISPATCH(D, CAUSAL, BF, FN, ...)                                                              \
+  (layout_dim(D) == 64    ? SAGE_ATTN_DISPATCH_DL(64, CAUSAL, BF, FN, __VA_ARGS__)                              \
+   : layout_dim(D) == 128 ? SAGE_ATTN_DISPATCH_DL(128, CAUSAL, BF, FN, __VA_ARGS__)                             \
+                          : SAGE_ATTN_DISPATCH_DL(256, CAUSAL, BF, FN, __VA_ARGS__))
 
 int attn_plan_impl(int B, int H, int Sq, int Skv, int D, int causal, int* n_full, int* chunks, int64_t* ws) {
   int rc = check_attn_shape(B, H, H, Sq, Skv, D, causal, "sage_attn_plan");
@@ -563,7 +578,7 @@ int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* 
   SAGE_REQUIRE(osb % 8 == 0 && oss % 8 == 0 && osh % 8 == 0 && osb >= 0 && oss >= 0 && osh >= 0,
                "%s: out strides must be non-negative multiples of 8 elements", who);
   return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn, q8, qs, k8, ks, v8t, vs, out, osb,
-                            oss, osh, lse, B, H, Hkv, Sq, Skv, workspace, workspace_bytes, (hipStream_t)stream);
+                            oss, osh, lse, B, H, Hkv, Sq, Skv, D, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // namespace sage
@@ -573,11 +588,10 @@ namespace sage {
 template <int D, bool CAUSAL, int OUT_DT>
 static int launch_attn_varlen(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks,
                               const uint8_t* v8t, const float* vs, void* out, int64_t oss, int64_t osh, int H, int Hkv,
-                              int TQ, int TKP, int n_blocks, VarlenTiles vt, hipStream_t st) {
-  const float c0 = (float)((1.0 / __builtin_sqrt((double)D)) * 1.4426950408889634);
+                              int TQ, int TKP, int hd, int n_blocks, VarlenTiles vt, hipStream_t st) {
   hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
                      v8t, vs, static_cast<uint16_t*>(out), (int64_t)0, oss, osh, nullptr, H, Hkv, TQ, 0, TKP, 0,
-                     n_blocks, n_blocks, 1, nullptr, c0, vt);
+                     n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt);
   return check_launch("varlen attention launch");
 }
 
@@ -588,7 +602,7 @@ int attn_varlen_impl(const int8_t* q8, const float* qs, const int8_t* k8, const 
                      const int* kp, void* stream) {
   const VarlenTiles vt{static_cast<const int4*>(tiles), cu_q, cu_k, kp};
   return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn_varlen, q8, qs, k8, ks, v8t, vs, out,
-                            oss, osh, H, Hkv, TQ, TKP, n_blocks, vt, (hipStream_t)stream);
+                            oss, osh, H, Hkv, TQ, TKP, D, n_blocks, vt, (hipStream_t)stream);
 }
 
 }  // namespace sage

@@ -54,17 +54,21 @@ const char* sage_last_error(void) { return sage::g_err; }
 
 int sage_kv_pad(int skv) { return skv <= 0 ? 0 : sage::kv_pad(skv); }
 
+int sage_layout_dim(int head_dim) { return sage::head_dim_ok(head_dim) ? sage::layout_dim(head_dim) : 0; }
+
 const char* sage_manifest_json(void) {
-  return "{\"arch\": \"gfx950\", \"head_dims\": [64, 128], \"dtypes\": [\"bf16\", \"f16\"], "
+  return "{\"arch\": \"gfx950\", \"head_dims\": [64, 96, 128, 256], \"layout_dims\": [64, 128, 128, 256], "
+         "\"rotation_block\": [64, 0, 128, 128], \"dtypes\": [\"bf16\", \"f16\"], "
          "\"kv_block\": 32, \"kv_pad\": 128, "
          "\"quant_q\": {\"rows_per_block\": 64, \"threads\": 256, \"lanes_per_row\": 4, \"rotation\": \"fwht_f64\"}, "
          "\"quant_kv\": {\"rows_per_block\": 128, \"threads\": 256}, "
          "\"v_amax\": {\"rows_per_block\": 256, \"threads\": 256}, "
-         "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": 3, \"max_kv_chunks\": 16, "
+         "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": {\"d64\": 3, \"d128\": 3, \"d256\": 2}, "
+         "\"max_kv_chunks\": 16, "
          "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
-         "\"variants\": [\"d64\", \"d128\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
+         "\"variants\": [\"d64\", \"d128\", \"d256\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
          "\"varlen\": {\"meta_threads\": 1024, \"sort_bins\": 2048, \"kv_rows_per_sequence\": \"multiple of 128\"}, "
-         "\"lse\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"mfma\": \"v_mfma_f32_32x32x16_{bf16,f16}\", "
+         "\"lse\": {\"head_dims\": [64, 128], \"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"mfma\": \"v_mfma_f32_32x32x16_{bf16,f16}\", "
          "\"causal\": \"bottom-right, q_len <= kv_len\"}}";
 }
 
@@ -85,7 +89,8 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
   // validate everything before the first launch so a bad call leaves the stream untouched
   SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "sage_forward: sizes must be positive");
   SAGE_REQUIRE(H % Hkv == 0, "sage_forward: heads %d not a multiple of kv heads %d", H, Hkv);
-  if (D != 64 && D != 128) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 128)", D);
+  if (!sage::head_dim_ok(D))
+    return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 96, 128, 256)", D);
   if (causal && Sq > Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len <= kv_len");
   int rc;
   if (workspace == nullptr) {

@@ -137,6 +137,18 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float y) {
   return code | sign;
 }
 
+// ---- head dims --------------------------------------------------------------------------------------------------
+// Head dims of the path (kernel_build/build_kernels.py:26-41): power-of-two dims are rotated by a Hadamard block of
+// RB = min(D, 128) channels (block-diagonal for D = 256, kernel_build/sage_quant.py:18-30); D = 96 is not rotated
+// and its int8 / E4M3 rows are stored zero-padded to DP = 128 channels, so the d128 attention kernel runs it.
+template <int D> struct HeadDim {
+  static constexpr int DP = D == 96 ? 128 : D;                // channels of the Q8 / K8 / V8T / VS layouts
+  static constexpr bool ROT = (D & (D - 1)) == 0;             // Hadamard rotation
+  static constexpr int RB = D < 128 ? D : 128;                // rotation block
+  static constexpr int EPL = DP / 4;                          // elements per lane, 4 lanes per row
+  static constexpr int RLANES = ROT ? RB / EPL : 1;           // lanes per rotation block
+};
+
 // ---- misc -------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)(d & 0xFF) << 24);

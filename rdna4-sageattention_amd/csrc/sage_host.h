@@ -35,6 +35,10 @@ inline int check_launch(const char* what) {
   return SAGE_OK;
 }
 
+// head dims of the path, and the channel count of their int8 / E4M3 layouts (96 is stored zero-padded to 128)
+__host__ __device__ constexpr bool head_dim_ok(int d) { return d == 64 || d == 96 || d == 128 || d == 256; }
+__host__ __device__ constexpr int layout_dim(int d) { return d == 96 ? 128 : d; }
+
 // padded KV length used by every K8 / KS / V8T layout
 inline int kv_pad(int skv) { return (skv + SAGE_KV_PAD - 1) / SAGE_KV_PAD * SAGE_KV_PAD; }
 

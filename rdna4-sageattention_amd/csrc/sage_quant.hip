@@ -6,9 +6,13 @@
 //                   (values are >= 0, so unsigned order == float order)               (_attention.py:120-121)
 //  quant_kv_kernel  K rows -> Hadamard -> int8, one scale per 32 keys; V -> E4M3 with the per-channel scale,
 //                   transposed through LDS into V8T                                  (sage_quant.py:264-283)
+//  quant_qk_vamax_kernel, quant_v_kernel   the same work in sage_forward's two launches
+//  quant_varlen_kernel, quant_v_varlen_kernel   packed variable-length batches
 //
-// Row mapping of the Hadamard kernels: 4 lanes (one quad) per row, each lane owns D / 4 consecutive elements
-// (64 or 32 bytes of bf16 / fp16), so a wave64 rotates 16 rows at a time.
+// Row mapping of the Hadamard kernels: 4 lanes (one quad) per row, each lane owns DP / 4 consecutive elements
+// (32 to 128 bytes of bf16 / fp16), so a wave64 rotates 16 rows at a time.  Head dims 64 / 128 rotate over the whole
+// row, 256 over two 128-channel blocks (2 lanes each), 96 is not rotated and lane 3 holds the zero padding of its
+// 128-channel layout.
 #include "sage_common.h"
 #include "sage_host.h"
 
@@ -58,7 +62,8 @@ template <int D, int DT>
 __device__ __forceinline__ void quant_q_rows(const uint16_t* __restrict__ x, int64_t sb, int64_t ss, int64_t sh, int H,
                                              int S, int row_tiles, float qs_mul, int8_t* __restrict__ q8,
                                              float* __restrict__ qs, int block) {
-  constexpr int EPL = D / QUAD;
+  using HD = HeadDim<D>;
+  constexpr int EPL = HD::EPL;
   const int tile = block % row_tiles;
   const int bh = block / row_tiles;
   const int b = bh / H, h = bh % H;
@@ -66,11 +71,12 @@ __device__ __forceinline__ void quant_q_rows(const uint16_t* __restrict__ x, int
   const int j = lane & 3;
   const int row = tile * 64 + wave * 16 + (lane >> 2);
   const bool valid = row < S;
-  const uint16_t* src = x + b * sb + (int64_t)(valid ? row : 0) * ss + h * sh + j * EPL;
+  const bool has_ch = j * EPL < D;  // D = 96: lane 3 holds the zero padding of the 128-channel layout
+  const uint16_t* src = x + b * sb + (int64_t)(valid ? row : 0) * ss + h * sh + (has_ch ? j * EPL : 0);
 
   double xd[EPL];
-  load_row_slice<EPL, DT>(src, valid, xd);
-  fwht_f64<EPL, QUAD>(xd, j);
+  load_row_slice<EPL, DT>(src, valid && has_ch, xd);
+  if (HD::ROT) fwht_f64<EPL, HD::RLANES>(xd, j);
   float xf[EPL];
   float amax = 0.0f;
 #pragma unroll
@@ -81,9 +87,10 @@ __device__ __forceinline__ void quant_q_rows(const uint16_t* __restrict__ x, int
   amax = fmaxf(row_max<QUAD>(amax), 1e-12f);
   const float s = amax / 127.0f;
   const float r = 1.0f / s;
-  int8_t* dst = q8 + ((int64_t)bh * S + row) * D + j * EPL;
+  int8_t* dst = q8 + ((int64_t)bh * S + row) * HD::DP + j * EPL;
   quantize_store_i8<EPL>(xf, s, r, dst, valid);
-  if (valid && j == 0) qs[(int64_t)bh * S + row] = (s / (float)D) * qs_mul;
+  // the unnormalised rotation multiplies Q K^T by RB (sage_quant.py:259-260); no rotation, no division
+  if (valid && j == 0) qs[(int64_t)bh * S + row] = (HD::ROT ? s / (float)HD::RB : s) * qs_mul;
 }
 
 template <int D, int DT>
@@ -102,14 +109,17 @@ __global__ __launch_bounds__(256) void fill_kernel(float* __restrict__ p, int64_
 }
 
 // Per-channel max |v| over rows [row_beg, row_end) of one (batch, kv head): `base` points at channel 0 of row 0.
-// Returns the maximum of channel threadIdx.x in threads [0, D) (0 for an empty range).
+// Returns the maximum of channel threadIdx.x in threads [0, DP) (0 for an empty range and for the padding channels
+// of D = 96).
 template <int D, int DT>
 __device__ __forceinline__ float vamax_core(const uint16_t* __restrict__ base, int64_t ss, int row_beg, int row_end) {
-  constexpr int LPR = D / 8;      // lanes per row, 8 elements (16 bytes) each
+  constexpr int DP = HeadDim<D>::DP;
+  constexpr int LPR = DP / 8;     // lanes per row, 8 elements (16 bytes) each
   constexpr int RPI = 256 / LPR;  // rows per iteration
-  __shared__ float red[RPI][D + 1];
+  __shared__ float red[RPI][DP + 1];
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
   const uint16_t* cb = base + c8 * 8;
+  if (c8 * 8 >= D) row_end = row_beg;  // padding channels: nothing to load
   float m[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) m[i] = 0.0f;
@@ -136,7 +146,7 @@ __device__ __forceinline__ float vamax_core(const uint16_t* __restrict__ base, i
   for (int i = 0; i < 8; ++i) red[r0][c8 * 8 + i] = m[i];
   __syncthreads();
   float a = 0.0f;
-  if (threadIdx.x < D) {
+  if (threadIdx.x < DP) {
 #pragma unroll 8
     for (int r = 0; r < RPI; ++r) a = fmaxf(a, red[r][threadIdx.x]);
   }
@@ -144,7 +154,7 @@ __device__ __forceinline__ float vamax_core(const uint16_t* __restrict__ base, i
 }
 
 // One block reduces `chunk_rows` rows of one (batch, kv head) to per-channel max |v|.  PARTIAL: store the chunk's
-// maxima to out[(bh * chunks + chunk) * D + d]; otherwise combine into out[bh * D + d] with atomicMax on the fp32 bit
+// maxima to out[(bh * chunks + chunk) * DP + d]; otherwise combine into out[bh * DP + d] with atomicMax on the fp32 bit
 // pattern (values are >= 0, so unsigned order == float order; out must start at zero).
 template <int D, int DT, bool PARTIAL>
 __device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64_t sb, int64_t ss, int64_t sh,
@@ -153,12 +163,13 @@ __device__ __forceinline__ void vamax_rows(const uint16_t* __restrict__ v, int64
   const int chunk = block % chunks;
   const int bh = block / chunks;
   const int b = bh / Hkv, h = bh % Hkv;
+  constexpr int DP = HeadDim<D>::DP;
   const float a = vamax_core<D, DT>(v + b * sb + h * sh, ss, chunk * chunk_rows, min(S, (chunk + 1) * chunk_rows));
-  if (threadIdx.x < D) {
+  if (threadIdx.x < DP) {
     if (PARTIAL)
-      out[((int64_t)bh * chunks + chunk) * D + threadIdx.x] = a;
+      out[((int64_t)bh * chunks + chunk) * DP + threadIdx.x] = a;
     else
-      atomicMax(reinterpret_cast<unsigned int*>(out + (int64_t)bh * D + threadIdx.x), __float_as_uint(a));
+      atomicMax(reinterpret_cast<unsigned int*>(out + (int64_t)bh * DP + threadIdx.x), __float_as_uint(a));
   }
 }
 
@@ -174,70 +185,27 @@ constexpr int V_AMAX_ROWS = 512;  // keys per V-maxima chunk in sage_forward
 
 // ------------------------------------------------------------------------------------------------------------------
 // K: Hadamard -> int8 with one scale per 32 keys.
-//  quant_k_rows128: 128 keys per block, wave w quantizes keys [32w, 32w + 32) in two passes of 16 rows.
-//  quant_k_rows64:  64 keys per block, wave w rotates keys [16w, 16w + 16) and the two waves of a 32-key group
-//                   combine their maxima through LDS (half the registers of the two-pass form).
+//  64 keys per block, wave w rotates keys [16w, 16w + 16) and the two waves of a 32-key group combine their maxima
+//  through LDS.
 // ------------------------------------------------------------------------------------------------------------------
-template <int D, int DT>
-__device__ __forceinline__ void quant_k_rows128(const uint16_t* __restrict__ k, int64_t ksb, int64_t kss, int64_t ksh,
-                                                int Hkv, int S, int Skp, int8_t* __restrict__ k8,
-                                                float* __restrict__ ks, int block) {
-  constexpr int EPL = D / QUAD;
-  const int nblk = Skp / 128;
-  const int blk = block % nblk;
-  const int bh = block / nblk;
-  const int b = bh / Hkv, h = bh % Hkv;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int j = lane & 3;
-  // ---- K ----
-  float xf[2][EPL];
-  float amax = 0.0f;
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int row = blk * 128 + wave * 32 + p * 16 + (lane >> 2);
-    const bool valid = row < S;
-    const uint16_t* src = k + b * ksb + (int64_t)(valid ? row : 0) * kss + h * ksh + j * EPL;
-    double xd[EPL];
-    load_row_slice<EPL, DT>(src, valid, xd);
-    fwht_f64<EPL, QUAD>(xd, j);
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      xf[p][i] = (float)xd[i];
-      amax = fmaxf(amax, fabsf(xf[p][i]));
-    }
-  }
-  // max over the wave's 32 rows (64 lanes)
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  amax = fmaxf(amax, 1e-12f);
-  const float s = amax / 127.0f;
-  const float r = 1.0f / s;
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int row = blk * 128 + wave * 32 + p * 16 + (lane >> 2);
-    int8_t* dst = k8 + ((int64_t)bh * Skp + row) * D + j * EPL;
-    quantize_store_i8<EPL>(xf[p], s, r, dst, true);
-  }
-  if (lane == 0) ks[(int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 4 + wave] = s;
-
-}
-
 // 64 keys: local rows [local0, local0 + 64) of one (batch, kv head), `base` = row 0 of its source; rows >= nvalid
 // are zero.  Writes the 64 int8 rows at k8_blk and the two 32-key scales at ks_blk.
 template <int D, int DT>
 __device__ __forceinline__ void quant_k64_core(const uint16_t* __restrict__ base, int64_t kss, int local0, int nvalid,
                                                int8_t* __restrict__ k8_blk, float* __restrict__ ks_blk) {
-  constexpr int EPL = D / QUAD;
+  using HD = HeadDim<D>;
+  constexpr int EPL = HD::EPL;
   __shared__ float wave_max[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 3;
   const int r = wave * 16 + (lane >> 2);
   const int row = local0 + r;
   const bool valid = row < nvalid;
-  const uint16_t* src = base + (int64_t)(valid ? row : 0) * kss + j * EPL;
+  const bool has_ch = j * EPL < D;
+  const uint16_t* src = base + (int64_t)(valid ? row : 0) * kss + (has_ch ? j * EPL : 0);
   double xd[EPL];
-  load_row_slice<EPL, DT>(src, valid, xd);
-  fwht_f64<EPL, QUAD>(xd, j);
+  load_row_slice<EPL, DT>(src, valid && has_ch, xd);
+  if (HD::ROT) fwht_f64<EPL, HD::RLANES>(xd, j);
   float xf[EPL];
   float amax = 0.0f;
 #pragma unroll
@@ -252,8 +220,9 @@ __device__ __forceinline__ void quant_k64_core(const uint16_t* __restrict__ base
   amax = fmaxf(fmaxf(wave_max[wave & ~1], wave_max[wave | 1]), 1e-12f);
   const float s = amax / 127.0f;
   const float rs = 1.0f / s;
-  quantize_store_i8<EPL>(xf, s, rs, k8_blk + (int64_t)r * D + j * EPL, true);
+  quantize_store_i8<EPL>(xf, s, rs, k8_blk + (int64_t)r * HD::DP + j * EPL, true);
   if (lane == 0 && (wave & 1) == 0) ks_blk[wave >> 1] = s;
+  __syncthreads();  // wave_max may be reused by the next call in this workgroup
 }
 
 template <int D, int DT>
@@ -264,7 +233,7 @@ __device__ __forceinline__ void quant_k_rows64(const uint16_t* __restrict__ k, i
   const int blk = block % nblk;
   const int bh = block / nblk;
   const int b = bh / Hkv, h = bh % Hkv;
-  quant_k64_core<D, DT>(k + b * ksb + h * ksh, kss, blk * 64, S, k8 + ((int64_t)bh * Skp + blk * 64) * D,
+  quant_k64_core<D, DT>(k + b * ksb + h * ksh, kss, blk * 64, S, k8 + ((int64_t)bh * Skp + blk * 64) * HeadDim<D>::DP,
                         ks + (int64_t)bh * (Skp / SAGE_KV_BLOCK) + blk * 2);
 }
 
@@ -280,12 +249,14 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
                                                 const float* __restrict__ am_src, int vchunks,
                                                 float* __restrict__ vs_out, uint8_t* __restrict__ v8t_blk,
                                                 int64_t chan_stride) {
-  constexpr int PITCH = D + 4;  // LDS row pitch of the [128 keys][D] E4M3 staging tile
+  constexpr int DP = HeadDim<D>::DP;
+  constexpr int PITCH = DP + 4;  // LDS row pitch of the [128 keys][DP] E4M3 staging tile
   __shared__ uint8_t vtile[128 * PITCH];
   // ---- V: scale, E4M3, stage [key][d] in LDS ----
-  constexpr int LPR = D / 8;      // lanes per row (8 channels each)
+  constexpr int LPR = DP / 8;     // lanes per row (8 channels each)
   constexpr int RPI = 256 / LPR;  // rows per pass
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
+  if (c8 * 8 >= D) nvalid = 0;  // padding channels of D = 96: zeros
   float am[8];
   if (vchunks == 0) {
 #pragma unroll
@@ -294,7 +265,7 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
 #pragma unroll
     for (int i = 0; i < 8; ++i) am[i] = 0.0f;
     for (int c = 0; c < vchunks; ++c) {
-      const v4f* p4 = reinterpret_cast<const v4f*>(am_src + (int64_t)c * D + c8 * 8);
+      const v4f* p4 = reinterpret_cast<const v4f*>(am_src + (int64_t)c * DP + c8 * 8);
       const v4f a = p4[0], b4 = p4[1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -340,7 +311,7 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
 
   // ---- V: transposed store.  Thread -> (4-channel group cg, 16-key set ksel); key set ksel = 4G + u covers output
   // positions [64G + 16u, +16) of this 128-key block, i.e. keys 64G + 8g + 4h + r with h = u / 2, g = 4(u % 2) + i.
-  constexpr int NCG = D / 4;
+  constexpr int NCG = DP / 4;
   for (int item = threadIdx.x; item < NCG * 8; item += 256) {
     const int ksel = item % 8, cg = item / 8;
     const int G = ksel >> 2, u = ksel & 3, hh = u >> 1;
@@ -378,10 +349,11 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
   const int blk = block % nblk;
   const int bh = block / nblk;
   const int b = bh / Hkv, h = bh % Hkv;
-  const float* am_src = vs + (int64_t)bh * (vchunks == 0 ? 1 : vchunks) * D;
-  float* out_row = (vchunks > 0 && blk == 0) ? vs_out + (int64_t)bh * D : nullptr;
+  constexpr int DP = HeadDim<D>::DP;
+  const float* am_src = vs + (int64_t)bh * (vchunks == 0 ? 1 : vchunks) * DP;
+  float* out_row = (vchunks > 0 && blk == 0) ? vs_out + (int64_t)bh * DP : nullptr;
   quant_v128_core<D, DT>(v + b * vsb + h * vsh, vss, blk * 128, S, am_src, vchunks, out_row,
-                         v8t + (int64_t)bh * D * Skp + blk * 128, Skp);
+                         v8t + (int64_t)bh * DP * Skp + blk * 128, Skp);
 }
 
 // sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (V_AMAX_ROWS keys each) to `vpart`,
@@ -412,7 +384,8 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restric
                                                        int64_t vss, int64_t vsh, int Hkv, int S, int Skp,
                                                        const float* __restrict__ vs, int8_t* __restrict__ k8,
                                                        float* __restrict__ ks, uint8_t* __restrict__ v8t) {
-  quant_k_rows128<D, DT>(k, ksb, kss, ksh, Hkv, S, Skp, k8, ks, blockIdx.x);
+  quant_k_rows64<D, DT>(k, ksb, kss, ksh, Hkv, S, Skp, k8, ks, 2 * blockIdx.x);
+  quant_k_rows64<D, DT>(k, ksb, kss, ksh, Hkv, S, Skp, k8, ks, 2 * blockIdx.x + 1);
   quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vs, 0, nullptr, v8t, blockIdx.x);
 }
 
@@ -457,8 +430,9 @@ __global__ __launch_bounds__(256) void quant_varlen_kernel(const uint16_t* __res
     const int kb = vk.cu_k[seq], n = vk.cu_k[seq + 1] - kb, local0 = g * 128 - vk.kp[seq];
     if (local0 >= n) return;  // padding only
     const float a = vamax_core<D, DT>(v + h * vsh + (int64_t)kb * vss, vss, local0, min(n, local0 + 128));
-    if (threadIdx.x < D)
-      atomicMax(reinterpret_cast<unsigned int*>(vs + ((int64_t)seq * Hkv + h) * D + threadIdx.x), __float_as_uint(a));
+    if (threadIdx.x < HeadDim<D>::DP)
+      atomicMax(reinterpret_cast<unsigned int*>(vs + ((int64_t)seq * Hkv + h) * HeadDim<D>::DP + threadIdx.x),
+                __float_as_uint(a));
   } else if (blk < nv + nk) {
     const int i = blk - nv;
     const int g = i % (TKP / 64), h = i / (TKP / 64);
@@ -466,7 +440,7 @@ __global__ __launch_bounds__(256) void quant_varlen_kernel(const uint16_t* __res
     if (seq < 0) return;
     const int kb = vk.cu_k[seq];
     quant_k64_core<D, DT>(k + h * ksh + (int64_t)kb * kss, kss, g * 64 - vk.kp[seq], vk.cu_k[seq + 1] - kb,
-                          k8 + ((int64_t)h * TKP + g * 64) * D, ks + (int64_t)h * (TKP / SAGE_KV_BLOCK) + g * 2);
+                          k8 + ((int64_t)h * TKP + g * 64) * HeadDim<D>::DP, ks + (int64_t)h * (TKP / SAGE_KV_BLOCK) + g * 2);
   } else {
     quant_q_rows<D, DT>(x, 0, qss, qsh, H, TQ, row_tiles, qs_mul, q8, qs, blk - nv - nk);
   }
@@ -482,7 +456,8 @@ __global__ __launch_bounds__(256) void quant_v_varlen_kernel(const uint16_t* __r
   if (seq < 0) return;
   const int kb = vk.cu_k[seq];
   quant_v128_core<D, DT>(v + h * vsh + (int64_t)kb * vss, vss, g * 128 - vk.kp[seq], vk.cu_k[seq + 1] - kb,
-                         vs + ((int64_t)seq * Hkv + h) * D, 0, nullptr, v8t + (int64_t)h * D * TKP + g * 128, TKP);
+                         vs + ((int64_t)seq * Hkv + h) * HeadDim<D>::DP, 0, nullptr,
+                         v8t + (int64_t)h * HeadDim<D>::DP * TKP + g * 128, TKP);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -490,7 +465,7 @@ __global__ __launch_bounds__(256) void quant_v_varlen_kernel(const uint16_t* __r
 // ------------------------------------------------------------------------------------------------------------------
 static int check_common(int B, int H, int S, int D, int dtype, const char* who) {
   SAGE_REQUIRE(B > 0 && H > 0 && S > 0, "%s: sizes must be positive (B=%d H=%d S=%d)", who, B, H, S);
-  if (D != 64 && D != 128) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 128)", who, D);
+  if (!head_dim_ok(D)) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 96, 128, 256)", who, D);
   if (dtype != SAGE_DTYPE_BF16 && dtype != SAGE_DTYPE_F16)
     return fail(SAGE_ERR_UNSUPPORTED, "%s: dtype code %d (bf16=0, f16=1)", who, dtype);
   return SAGE_OK;
@@ -516,7 +491,7 @@ static void launch_quant_q(const void* q, int64_t sb, int64_t ss, int64_t sh, in
 template <int D, int DT>
 static void launch_v_amax(const void* v, int64_t sb, int64_t ss, int64_t sh, int B, int Hkv, int S, float* vs,
                           hipStream_t st) {
-  const int64_t n = (int64_t)B * Hkv * D;
+  const int64_t n = (int64_t)B * Hkv * HeadDim<D>::DP;
   hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, vs, n, 0.0f);
   // aim for ~256 rows per block, but keep the block count per (b, h) bounded
   int chunk_rows = 256;
@@ -569,12 +544,15 @@ static void launch_varlen_quant(const void* q, int64_t qss, int64_t qsh, const v
                      vss, vsh, Hkv, TKP, vk, vs, v8t);
 }
 
-#define SAGE_DISPATCH_D_DT(D, DT, FN, ...)                                      \
-  do {                                                                        \
-    if ((D) == 64 && (DT) == SAGE_DTYPE_BF16) FN<64, DT_BF16>(__VA_ARGS__);    \
-    else if ((D) == 64) FN<64, DT_F16>(__VA_ARGS__);                            \
-    else if ((DT) == SAGE_DTYPE_BF16) FN<128, DT_BF16>(__VA_ARGS__);           \
-    else FN<128, DT_F16>(__VA_ARGS__);                                        \
+#define SAGE_DISPATCH_D_DT(D, DT, FN, ...)                                                   \
+  do {                                                                                     \
+    const bool bf_ = (DT) == SAGE_DTYPE_BF16;                                              \
+    switch (D) {                                                                           \
+      case 64: bf_ ? FN<64, DT_BF16>(__VA_ARGS__) : FN<64, DT_F16>(__VA_ARGS__); break;     \
+      case 96: bf_ ? FN<96, DT_BF16>(__VA_ARGS__) : FN<96, DT_F16>(__VA_ARGS__); break;     \
+      case 128: bf_ ? FN<128, DT_BF16>(__VA_ARGS__) : FN<128, DT_F16>(__VA_ARGS__); break;  \
+      default: bf_ ? FN<256, DT_BF16>(__VA_ARGS__) : FN<256, DT_F16>(__VA_ARGS__); break;   \
+    }                                                                                      \
   } while (0)
 
 int quant_q_impl(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H, int Sq, int D, int dtype,
@@ -616,7 +594,7 @@ int quant_kv_impl(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const vo
 }
 
 int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D) {
-  return (int64_t)B * Hkv * ((Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS) * D * (int64_t)sizeof(float);
+  return (int64_t)B * Hkv * ((Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS) * layout_dim(D) * (int64_t)sizeof(float);
 }
 
 // Validation of every argument is done by the caller (sage_forward) through the per-stage checks below.

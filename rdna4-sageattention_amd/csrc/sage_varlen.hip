@@ -257,7 +257,8 @@ int sage_forward_varlen(const void* q, int64_t qss, int64_t qsh, const void* k, 
   sage::VarlenLayout L;
   int rc = sage::varlen_layout(batch, H, Hkv, total_q, total_k, &L);
   if (rc) return rc;
-  if (D != 64 && D != 128) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward_varlen: head_dim %d (supported 64, 128)", D);
+  if (!sage::head_dim_ok(D))
+    return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward_varlen: head_dim %d (supported 64, 96, 128, 256)", D);
   if (dtype != SAGE_DTYPE_BF16 && dtype != SAGE_DTYPE_F16)
     return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward_varlen: dtype code %d (bf16=0, f16=1)", dtype);
   if ((rc = sage::check_packed(q, qss, qsh, "q"))) return rc;
@@ -285,7 +286,7 @@ int sage_forward_varlen(const void* q, int64_t qss, int64_t qsh, const void* k, 
                      cu_seqlens_k, batch, H, total_q, total_k, hdr, kp, order, tpre);
   if ((rc = sage::check_launch("varlen meta launch"))) return rc;
   const int n_kblk = L.tkp / 128;
-  const int64_t n_vs = (int64_t)batch * Hkv * D;
+  const int64_t n_vs = (int64_t)batch * Hkv * sage::layout_dim(D);
   const int64_t n_items = std::max<int64_t>(std::max(L.n_blocks, n_kblk), n_vs);
   const int grid = (int)std::min<int64_t>((n_items + 255) / 256, 4096);
   hipLaunchKernelGGL(sage::varlen_prep_kernel, dim3(grid), dim3(256), 0, st, hdr, cu_seqlens_q, kp, order, tpre, batch,

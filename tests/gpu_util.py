@@ -24,7 +24,8 @@ def run_quant_q(q: torch.Tensor, layout="HND", qs_mul=1.0):
         B, H, S, D = q.shape
     else:
         B, S, H, D = q.shape
-    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
+    dl = _capi.layout_dim(D)
+    q8 = torch.empty(B, H, S, dl, dtype=torch.int8, device=dev)
     qs = torch.empty(B, H, S, dtype=torch.float32, device=dev)
     _capi.call("sage_quant_q", q.data_ptr(), *bsh(q, layout), B, H, S, D, DT[q.dtype], qs_mul, q8.data_ptr(),
                qs.data_ptr(), stream(dev))
@@ -39,10 +40,11 @@ def run_quant_kv(k: torch.Tensor, v: torch.Tensor, layout="HND"):
     else:
         B, S, Hkv, D = k.shape
     skp = _capi.kv_pad(S)
-    vs = torch.empty(B, Hkv, D, dtype=torch.float32, device=dev)
-    k8 = torch.empty(B, Hkv, skp, D, dtype=torch.int8, device=dev)
+    dl = _capi.layout_dim(D)
+    vs = torch.empty(B, Hkv, dl, dtype=torch.float32, device=dev)
+    k8 = torch.empty(B, Hkv, skp, dl, dtype=torch.int8, device=dev)
     ks = torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev)
-    v8t = torch.empty(B, Hkv, D, skp, dtype=torch.uint8, device=dev)
+    v8t = torch.empty(B, Hkv, dl, skp, dtype=torch.uint8, device=dev)
     st = stream(dev)
     _capi.call("sage_v_amax", v.data_ptr(), *bsh(v, layout), B, Hkv, S, D, DT[v.dtype], vs.data_ptr(), st)
     _capi.call("sage_quant_kv", k.data_ptr(), *bsh(k, layout), v.data_ptr(), *bsh(v, layout), B, Hkv, S, D,
@@ -74,3 +76,11 @@ def kv_split(dev, B, H, Sq, Skv, D, causal, heads=None):
     if chunks <= 1:
         return None
     return chunks, orc.split_rows(B, H, Sq, n_full, heads=heads)
+
+
+def unpad(a: np.ndarray, d: int, axis: int = -1) -> np.ndarray:
+    """The first d channels of a layout array along `axis`; asserts the padding channels (head_dim 96 is stored as
+    128 channels) are zero."""
+    a = np.moveaxis(np.asarray(a), axis, -1)
+    assert not np.any(a[..., d:]), "padding channels must be zero"
+    return np.moveaxis(a[..., :d], -1, axis)

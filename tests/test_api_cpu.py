@@ -40,7 +40,7 @@ def test_api_surface():
     for mod in (cdna4_sage, rdna4_sage):
         for n in ["sageattn", "attention", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]:
             assert hasattr(mod, n), (mod, n)
-    assert cdna4_sage.ARCHS == ("gfx950",) and cdna4_sage.HEAD_DIMS == (64, 128)
+    assert cdna4_sage.ARCHS == ("gfx950",) and cdna4_sage.HEAD_DIMS == (64, 96, 128, 256)
     assert hasattr(torch.ops.cdna4_sage, "attention") and hasattr(torch.ops.rdna4_sage, "attention")
 
 

@@ -40,7 +40,7 @@ def test_abi_version_kv_pad_and_manifest():
     built = json.loads(lib.sage_manifest_json().decode())
     committed = json.loads((ROOT / "rdna4-sageattention_amd" / "cdna4_sage" / "manifest.json").read_text())
     assert {k: v for k, v in committed.items() if k not in ("library", "build_flags")} == built
-    assert built["arch"] == "gfx950" and built["head_dims"] == [64, 128] and built["kv_block"] == 32
+    assert built["arch"] == "gfx950" and built["head_dims"] == [64, 96, 128, 256] and built["kv_block"] == 32
 
 
 def _err():
@@ -52,8 +52,9 @@ def test_quant_q_validation():
     ok = (P, 128 * 64, 128, 64, 1, 2, 64, 128, 0, 1.0, P, P, None)   # noqa: F841 (shape of a valid call)
     assert lib.sage_quant_q(None, 0, 128, 0, 1, 1, 64, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
     assert "q is NULL" in _err()
-    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 64, 96, 0, 1.0, P, P, None) == _capi.SAGE_ERR_UNSUPPORTED
-    assert "head_dim 96" in _err()
+    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 64, 80, 0, 1.0, P, P, None) == _capi.SAGE_ERR_UNSUPPORTED
+    assert "head_dim 80" in _err()
+    assert [_capi.layout_dim(d) for d in (64, 96, 128, 256, 80, 0)] == [64, 128, 128, 256, 0, 0]
     assert lib.sage_quant_q(P + 2, 0, 128, 0, 1, 1, 64, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
     assert "aligned" in _err()
     assert lib.sage_quant_q(P, 0, 100, 0, 1, 1, 64, 128, 0, 1.0, P, P, None) == _capi.SAGE_ERR_INVALID
@@ -77,14 +78,14 @@ def test_kv_and_attention_validation():
 
     assert attn(H=3) == _capi.SAGE_ERR_INVALID and "multiple" in _err()
     assert attn(causal=1, Sq=65) == _capi.SAGE_ERR_UNSUPPORTED and "q_len <= kv_len" in _err()
-    assert attn(D=256) == _capi.SAGE_ERR_UNSUPPORTED
+    assert attn(D=80) == _capi.SAGE_ERR_UNSUPPORTED
     assert attn(out_dtype=3) == _capi.SAGE_ERR_UNSUPPORTED
     assert attn(q8=None) == _capi.SAGE_ERR_INVALID
     assert attn(oss=100) == _capi.SAGE_ERR_INVALID
     assert attn(Sq=0) == _capi.SAGE_ERR_INVALID
     n_full, chunks, ws = ctypes.c_int(-1), ctypes.c_int(-1), ctypes.c_int64(-1)
     refs = (ctypes.byref(n_full), ctypes.byref(chunks), ctypes.byref(ws))
-    assert lib.sage_attn_plan(1, 4, 64, 64, 96, 0, *refs) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 96" in _err()
+    assert lib.sage_attn_plan(1, 4, 64, 64, 80, 0, *refs) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 80" in _err()
     assert lib.sage_attn_plan(1, 4, 65, 64, 128, 1, *refs) == _capi.SAGE_ERR_UNSUPPORTED
     assert lib.sage_attn_plan(0, 4, 64, 64, 128, 0, *refs) == _capi.SAGE_ERR_INVALID
     assert (n_full.value, chunks.value, ws.value) == (-1, -1, -1)       # outputs untouched on error
@@ -140,7 +141,7 @@ def test_varlen_validates_before_launching():
         a = dict(args, **kw)
         return lib.sage_forward_varlen(*a.values())
 
-    assert call(D=96) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 96" in _err()
+    assert call(D=80) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 80" in _err()
     assert call(dtype=2) == _capi.SAGE_ERR_UNSUPPORTED
     assert call(Hkv=3) == _capi.SAGE_ERR_INVALID
     assert call(q=P + 8) == _capi.SAGE_ERR_INVALID and "16-byte" in _err()

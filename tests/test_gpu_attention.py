@@ -29,6 +29,11 @@ CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 8, 8, 1024, 1024, 64, torch.bfloat16, "HND", False),   # config 1 shape
     (1, 2, 2, 130, 777, 128, torch.float16, "HND", True),      # bottom-right causal, q_len < kv_len
     (2, 4, 2, 300, 1000, 64, torch.bfloat16, "NHD", True),
+    (1, 2, 2, 300, 300, 96, torch.bfloat16, "HND", False),     # head_dim 96: no rotation, 128-channel layout
+    (1, 4, 2, 257, 600, 96, torch.float16, "NHD", True),
+    (1, 2, 2, 300, 500, 256, torch.bfloat16, "HND", False),    # head_dim 256: block-diagonal rotation
+    (2, 2, 1, 200, 200, 256, torch.float16, "NHD", True),
+    (1, 8, 8, 1024, 1024, 256, torch.bfloat16, "HND", False),  # several split key ranges
 ]
 
 
@@ -145,7 +150,7 @@ def test_split_merge_is_deterministic_across_calls(dev):
     assert not torch.equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("D", [96, 256])
+@pytest.mark.parametrize("D", [80, 512])
 def test_unsupported_head_dims(dev, D):
     q = torch.randn(1, 2, 256, D, device=dev, dtype=torch.bfloat16)
     with pytest.raises(cdna4_sage.Unsupported):

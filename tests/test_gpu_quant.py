@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from gpu_util import DT as DT_CODE
-from gpu_util import bits, hnd_np, run_quant_kv, run_quant_q
+from gpu_util import bits, hnd_np, run_quant_kv, run_quant_q, unpad
 from oracle import sage_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -16,6 +16,8 @@ Q_CASES = [  # B, H, S, D, dtype, layout
     (1, 2, 4099, 64, torch.bfloat16, "NHD"),
     (2, 5, 130, 128, torch.float16, "HND"),
     (1, 24, 4608, 128, torch.bfloat16, "HND"),   # config 2 (Flux) at full size
+    (1, 3, 333, 96, torch.bfloat16, "NHD"),      # no rotation, stored as 128 channels
+    (2, 2, 129, 256, torch.float16, "HND"),      # two 128-channel Hadamard blocks
 ]
 
 
@@ -31,6 +33,7 @@ def _randn(shape, dtype, seed, layout="HND", scale=1.0):
 def test_quant_q_bitexact(dev, B, H, S, D, dt, layout):
     q = _randn((B, H, S, D), dt, 11 + S, layout)
     q8, qs = run_quant_q(q.to(dev), layout)
+    q8 = unpad(q8, D)
     e8, es = orc.quant_q(hnd_np(q, layout))
     assert np.array_equal(q8, e8), f"Q8 mismatch at {np.argwhere(q8 != e8)[:5]}"
     assert np.array_equal(bits(qs), bits(es))
@@ -51,6 +54,8 @@ KV_CASES = [  # B, Hkv, S, D, dtype, layout
     (1, 2, 1031, 64, torch.bfloat16, "HND"),
     (2, 2, 257, 128, torch.float16, "NHD"),
     (1, 24, 4608, 128, torch.bfloat16, "HND"),   # config 2 (Flux) at full size
+    (2, 2, 300, 96, torch.float16, "HND"),
+    (1, 3, 777, 256, torch.bfloat16, "NHD"),
 ]
 
 
@@ -59,6 +64,7 @@ def test_quant_kv_bitexact(dev, B, H, S, D, dt, layout):
     k = _randn((B, H, S, D), dt, 21 + S, layout)
     v = _randn((B, H, S, D), dt, 31 + S, layout, scale=2.0)
     k8, ks, v8t, vs = run_quant_kv(k.to(dev), v.to(dev), layout)
+    k8, v8t, vs = unpad(k8, D), unpad(v8t, D, axis=2), unpad(vs, D)
     skp = k8.shape[2]
     e8, eks, ev8, evs = orc.quant_kv(hnd_np(k, layout), hnd_np(v, layout), seq_pad=skp)
     assert np.array_equal(bits(vs), bits(evs)), "VS mismatch"
@@ -130,6 +136,8 @@ FWD_CASES = [  # B, H, Hkv, S, D, dtype
     (2, 4, 2, 515, 64, torch.float16),
     (1, 3, 1, 77, 128, torch.bfloat16),
     (1, 24, 24, 4608, 128, torch.bfloat16),   # config 2 (Flux): 9 chunks of V maxima
+    (1, 4, 2, 600, 96, torch.bfloat16),
+    (1, 2, 2, 1100, 256, torch.float16),
 ]
 
 
@@ -143,12 +151,13 @@ def test_forward_intermediates_bitexact(dev, B, H, Hkv, S, D, dt, with_workspace
     k = _randn((B, Hkv, S, D), dt, 4 + S).to(dev)
     v = _randn((B, Hkv, S, D), dt, 5 + S, scale=3.0).to(dev)
     skp = _capi.kv_pad(S)
-    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
+    dl = _capi.layout_dim(D)
+    q8 = torch.full((B, H, S, dl), 5, dtype=torch.int8, device=dev)      # stale values must be overwritten
     qs = torch.empty(B, H, S, dtype=torch.float32, device=dev)
-    k8 = torch.empty(B, Hkv, skp, D, dtype=torch.int8, device=dev)
+    k8 = torch.full((B, Hkv, skp, dl), 5, dtype=torch.int8, device=dev)
     ks = torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev)
-    v8t = torch.empty(B, Hkv, D, skp, dtype=torch.uint8, device=dev)
-    vs = torch.full((B, Hkv, D), 7.0, dtype=torch.float32, device=dev)    # stale values must be overwritten
+    v8t = torch.full((B, Hkv, dl, skp), 5, dtype=torch.uint8, device=dev)
+    vs = torch.full((B, Hkv, dl), 7.0, dtype=torch.float32, device=dev)
     out = torch.empty(B, S, H, D, dtype=dt, device=dev)
     wsb = _capi.forward_workspace(dev.index or 0, B, H, Hkv, S, S, D, False) if with_workspace else 0
     ws = torch.full((max(wsb, 1),), 0xFF, dtype=torch.uint8, device=dev)
@@ -160,8 +169,8 @@ def test_forward_intermediates_bitexact(dev, B, H, Hkv, S, D, dt, with_workspace
     torch.cuda.synchronize(dev)
     eq8, eqs = orc.quant_q(hnd_np(q.cpu()))
     ek8, eks, ev8, evs = orc.quant_kv(hnd_np(k.cpu()), hnd_np(v.cpu()), seq_pad=skp)
-    assert np.array_equal(q8.cpu().numpy(), eq8) and np.array_equal(bits(qs.cpu().numpy()), bits(eqs))
-    assert np.array_equal(bits(vs.cpu().numpy()), bits(evs)), "VS mismatch"
-    assert np.array_equal(k8.cpu().numpy(), ek8) and np.array_equal(bits(ks.cpu().numpy()), bits(eks))
-    assert np.array_equal(v8t.cpu().numpy(), orc.v8_to_device_layout(ev8)), "V8T mismatch"
+    assert np.array_equal(unpad(q8.cpu().numpy(), D), eq8) and np.array_equal(bits(qs.cpu().numpy()), bits(eqs))
+    assert np.array_equal(bits(unpad(vs.cpu().numpy(), D)), bits(evs)), "VS mismatch"
+    assert np.array_equal(unpad(k8.cpu().numpy(), D), ek8) and np.array_equal(bits(ks.cpu().numpy()), bits(eks))
+    assert np.array_equal(unpad(v8t.cpu().numpy(), D, axis=2), orc.v8_to_device_layout(ev8)), "V8T mismatch"
     assert torch.isfinite(out.float()).all()

@@ -38,12 +38,13 @@ def _varlen_capi(q, k, v, cu_q, cu_k, causal, out=None):
     TK, Hkv = k.shape[0], k.shape[1]
     batch = len(cu_q) - 1
     tkp, wsb = _capi.varlen_layout(batch, H, Hkv, TQ, TK)
-    r = dict(q8=torch.empty(H, TQ, D, dtype=torch.int8, device=dev),
+    dl = _capi.layout_dim(D)
+    r = dict(q8=torch.empty(H, TQ, dl, dtype=torch.int8, device=dev),
              qs=torch.empty(H, TQ, dtype=torch.float32, device=dev),
-             k8=torch.empty(Hkv, tkp, D, dtype=torch.int8, device=dev),
+             k8=torch.empty(Hkv, tkp, dl, dtype=torch.int8, device=dev),
              ks=torch.empty(Hkv, tkp // 32, dtype=torch.float32, device=dev),
-             v8t=torch.empty(Hkv, D, tkp, dtype=torch.uint8, device=dev),
-             vs=torch.empty(batch, Hkv, D, dtype=torch.float32, device=dev),
+             v8t=torch.empty(Hkv, dl, tkp, dtype=torch.uint8, device=dev),
+             vs=torch.empty(batch, Hkv, dl, dtype=torch.float32, device=dev),
              ws=torch.empty(wsb, dtype=torch.uint8, device=dev),
              out=torch.empty(TQ, H, D, dtype=q.dtype, device=dev) if out is None else out)
     cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
@@ -63,12 +64,13 @@ def _dense_capi(qi, ki, vi, causal):
     Sq, H, D = qi.shape
     Skv, Hkv = ki.shape[0], ki.shape[1]
     skp = _capi.kv_pad(Skv)
-    r = dict(q8=torch.empty(1, H, Sq, D, dtype=torch.int8, device=dev),
+    dl = _capi.layout_dim(D)
+    r = dict(q8=torch.empty(1, H, Sq, dl, dtype=torch.int8, device=dev),
              qs=torch.empty(1, H, Sq, dtype=torch.float32, device=dev),
-             k8=torch.empty(1, Hkv, skp, D, dtype=torch.int8, device=dev),
+             k8=torch.empty(1, Hkv, skp, dl, dtype=torch.int8, device=dev),
              ks=torch.empty(1, Hkv, skp // 32, dtype=torch.float32, device=dev),
-             v8t=torch.empty(1, Hkv, D, skp, dtype=torch.uint8, device=dev),
-             vs=torch.empty(1, Hkv, D, dtype=torch.float32, device=dev),
+             v8t=torch.empty(1, Hkv, dl, skp, dtype=torch.uint8, device=dev),
+             vs=torch.empty(1, Hkv, dl, dtype=torch.float32, device=dev),
              out=torch.empty(1, Sq, H, D, dtype=qi.dtype, device=dev))
     o = r["out"]
     _capi.call("sage_forward", qi.data_ptr(), 0, qi.stride(0), qi.stride(1), ki.data_ptr(), 0, ki.stride(0),
@@ -133,6 +135,8 @@ VARLEN_CASES = [  # lq, lk, H, Hkv, D, dtype, causal
     ([257, 100, 40, 513], [257, 300, 20, 513], 4, 1, 64, torch.float16, True),     # sequence 2: q_len > kv_len
     ([64, 200, 33], [128, 0, 1000], 2, 2, 128, torch.bfloat16, True),            # sequence 1 has no keys
     ([1000, 3, 1], [1000, 3, 1], 8, 8, 64, torch.bfloat16, False),
+    ([300, 90, 700], [500, 90, 650], 4, 2, 96, torch.bfloat16, True),
+    ([200, 333], [260, 700], 2, 1, 256, torch.float16, False),
 ]
 
 

@@ -154,6 +154,49 @@ def test_quant_q_invariants():
     assert np.all(q8[0, 0, 4] == 0) and qs[0, 0, 4] == F32(F32(F32(1e-12) / F32(127)) / F32(128))
 
 
+def test_rotation_by_head_dim():
+    """head_dim 256 rotates each 128-channel half by H128 (block-diagonal, x @ diag(H, H)); 96 is not rotated;
+    64 / 128 use the full-order matrix.  Integer rows keep every float64 sum exact, so equality is exact."""
+    rng = np.random.default_rng(9)
+    for d, rb in ((64, 64), (96, 0), (128, 128), (256, 128)):
+        assert orc.rotation_block(d) == rb
+        x = rng.integers(-40, 40, size=(5, d)).astype(np.float64)
+        if rb == 0:
+            expect = x
+        else:
+            h = orc.hadamard_pm1(rb)
+            expect = np.concatenate([x[:, i:i + rb] @ h for i in range(0, d, rb)], axis=1)
+        assert np.array_equal(orc.rotate_rows(x), expect), d
+
+
+@pytest.mark.parametrize("d", [96, 256])
+def test_quant_q_invariants_other_head_dims(d):
+    """QS = s / RB with RB = 128 for d256 (each block multiplies its share of Q K^T by 128), QS = s for d96."""
+    q = _bf16((1, 2, 70, d), 60 + d)
+    q8, qs = orc.quant_q(q)
+    x = orc.rotate_rows(q).astype(F32)
+    amax = np.abs(x).max(-1)
+    assert np.all(np.abs(q8.astype(int)).max(-1) == 127)
+    s = qs * (128 if d == 256 else 1)
+    assert np.allclose(s * 127, amax, rtol=1e-6)
+    if d == 96:
+        assert np.allclose(s * 127, np.abs(q).max(-1), rtol=1e-6)   # the raw row's max: no rotation
+    assert np.all(np.abs(q8 * s[..., None] - x) <= s[..., None] * 0.5 * (1 + 1e-5))
+    # the scores the kernel sees: Q8 K8^T * QS * KS equals Q K^T up to quantization error, for both head dims
+    k = _bf16((1, 2, 64, d), 61 + d)
+    k8, ks, _, _ = orc.quant_kv(k, k)
+    sc = (q8.astype(np.float64) @ np.swapaxes(k8, -1, -2).astype(np.float64)) * qs[..., None] * np.repeat(ks, 32, -1)[:, :, None, :64]
+    ref = q.astype(np.float64) @ np.swapaxes(k, -1, -2).astype(np.float64)
+    assert np.abs(sc - ref).max() <= 0.02 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("d,causal", [(96, False), (96, True), (256, False), (256, True)])
+def test_emulation_other_head_dims_vs_float64(d, causal):
+    q, k, v = _bf16((1, 2, 200, d), 70 + d), _bf16((1, 2, 200, d), 71 + d), _bf16((1, 2, 200, d), 72 + d)
+    out = orc.sage_forward(q, k, v, causal=causal, block_n=64)
+    assert _cos(out, orc.sdpa_reference(q, k, v, causal=causal)) >= 0.999
+
+
 def test_quant_kv_invariants_and_vector_norm():
     k = _bf16((1, 2, 100, 64), 7)
     v = _bf16((1, 2, 100, 64), 8, 3.0)
