@@ -66,7 +66,7 @@ def lib():
             if _lib is None:
                 if not LIB_PATH.exists():
                     raise RuntimeError(f"cdna4_sage: {LIB_PATH} is missing; build it with "
-                                       "`python -m cdna4_sage._build` (hipcc --offload-arch=gfx950)")
+                                       "`python rdna4-sageattention_amd/build_kernels.py` (hipcc --offload-arch=gfx950)")
                 h = ctypes.CDLL(str(LIB_PATH))
                 for name, (args, res) in SIGNATURES.items():
                     fn = getattr(h, name)
