@@ -20,12 +20,26 @@ namespace sage {
 
 constexpr int QUAD = 4;
 
-// Load EPL consecutive 16-bit elements (EPL * 2 bytes, 16-byte aligned) and widen them to float64.
+// 16 bytes from p, or zeros when !valid.  p must be dereferenceable either way (callers point invalid lanes at a
+// valid row).  The load is unconditional and the zeroing a bitwise AND: with a select the compiler sinks the load
+// into a branch, and a run of such loads then becomes one branch and one wait per load instead of all in flight.
+__device__ __forceinline__ uint4 load16_or_zero(const void* p, bool valid) {
+  uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint32_t m = 0u - (uint32_t)valid;
+  w.x &= m;
+  w.y &= m;
+  w.z &= m;
+  w.w &= m;
+  return w;
+}
+
+// Load EPL consecutive 16-bit elements (EPL * 2 bytes, 16-byte aligned; src dereferenceable even when !valid) and
+// widen them to float64 (zeros when !valid).
 template <int EPL, int DT>
 __device__ __forceinline__ void load_row_slice(const uint16_t* __restrict__ src, bool valid, double (&x)[EPL]) {
 #pragma unroll
   for (int k = 0; k < EPL / 8; ++k) {
-    uint4 w = valid ? *reinterpret_cast<const uint4*>(src + 8 * k) : make_uint4(0, 0, 0, 0);
+    const uint4 w = load16_or_zero(src + 8 * k, valid);
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -130,7 +144,7 @@ __device__ __forceinline__ float vamax_core(const uint16_t* __restrict__ base, i
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int row = row0 + g * RPI;
-      w[g] = row < row_end ? *reinterpret_cast<const uint4*>(cb + (int64_t)row * ss) : make_uint4(0, 0, 0, 0);
+      w[g] = load16_or_zero(cb + (int64_t)(row < row_end ? row : row0) * ss, row < row_end);  // row0 < row_end
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -181,7 +195,12 @@ __global__ __launch_bounds__(256) void v_amax_kernel(const uint16_t* __restrict_
   vamax_rows<D, DT, false>(v, sb, ss, sh, Hkv, S, chunks, chunk_rows, vs, blockIdx.x);
 }
 
-constexpr int V_AMAX_ROWS = 512;  // keys per V-maxima chunk in sage_forward
+// sage_forward's per-chunk V maxima: chunks of at least V_AMAX_ROWS keys, at most V_AMAX_CHUNKS per (batch, kv head),
+// so every V block of the second launch reduces at most 16 rows of maxima
+constexpr int V_AMAX_ROWS = 512;
+constexpr int V_AMAX_CHUNKS = 16;
+__host__ __device__ inline int vamax_chunks(int skv) { return min((skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS, V_AMAX_CHUNKS); }
+__host__ __device__ inline int vamax_chunk_rows(int skv) { return (skv + vamax_chunks(skv) - 1) / vamax_chunks(skv); }
 
 // ------------------------------------------------------------------------------------------------------------------
 // K: Hadamard -> int8 with one scale per 32 keys.
@@ -257,6 +276,15 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
   constexpr int RPI = 256 / LPR;  // rows per pass
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
   if (c8 * 8 >= D) nvalid = 0;  // padding channels of D = 96: zeros
+  // all of the thread's 128 / RPI rows in flight first: they do not depend on the channel maxima reduced below
+  const uint16_t* vbase = base + c8 * 8;
+  uint4 wv[128 / RPI];
+#pragma unroll
+  for (int g = 0; g < 128 / RPI; ++g) {
+    const int row = local0 + r0 + g * RPI;
+    const bool ok = row < nvalid;
+    wv[g] = load16_or_zero(ok ? vbase + (int64_t)row * vss : base, ok);  // base: row 0, channel 0 of the sequence
+  }
   float am[8];
   if (vchunks == 0) {
 #pragma unroll
@@ -264,13 +292,21 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) am[i] = 0.0f;
-    for (int c = 0; c < vchunks; ++c) {
-      const v4f* p4 = reinterpret_cast<const v4f*>(am_src + (int64_t)c * DP + c8 * 8);
-      const v4f a = p4[0], b4 = p4[1];
+    // all (at most V_AMAX_CHUNKS) rows of maxima in flight at once; indices past the last chunk repeat it, which a
+    // max does not notice
+    v4f pa[V_AMAX_CHUNKS], pb[V_AMAX_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < V_AMAX_CHUNKS; ++c) {
+      const v4f* p4 = reinterpret_cast<const v4f*>(am_src + (int64_t)min(c, vchunks - 1) * DP + c8 * 8);
+      pa[c] = p4[0];
+      pb[c] = p4[1];
+    }
+#pragma unroll
+    for (int c = 0; c < V_AMAX_CHUNKS; ++c) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        am[i] = fmaxf(am[i], a[i]);
-        am[4 + i] = fmaxf(am[4 + i], b4[i]);
+        am[i] = fmaxf(am[i], pa[c][i]);
+        am[4 + i] = fmaxf(am[4 + i], pb[c][i]);
       }
     }
     if (vs_out != nullptr && r0 == 0) {
@@ -282,14 +318,6 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
   float cs[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) cs[i] = 448.0f / fmaxf(am[i], 1e-30f);
-  const uint16_t* vbase = base + c8 * 8;
-  // all of the thread's 128 / RPI rows in flight before the first conversion
-  uint4 wv[128 / RPI];
-#pragma unroll
-  for (int g = 0; g < 128 / RPI; ++g) {
-    const int row = local0 + r0 + g * RPI;
-    wv[g] = row < nvalid ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * vss) : make_uint4(0, 0, 0, 0);
-  }
 #pragma unroll
   for (int g = 0; g < 128 / RPI; ++g) {
     const int rr = r0 + g * RPI;
@@ -356,7 +384,7 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
                          v8t + (int64_t)bh * DP * Skp + blk * 128, Skp);
 }
 
-// sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (V_AMAX_ROWS keys each) to `vpart`,
+// sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (vamax_chunk_rows keys each) to `vpart`,
 // blocks [nv, nv + nk) quantize 64 keys of K each, the rest quantize Q.  The V blocks come first so their longer row
 // loops start early.
 template <int D, int DT>
@@ -370,7 +398,7 @@ __global__ __launch_bounds__(256) void quant_qk_vamax_kernel(const uint16_t* __r
                                                              int vchunks, int nv, float* __restrict__ vpart) {
   const int blk = blockIdx.x;
   if (blk < nv)
-    vamax_rows<D, DT, true>(v, vsb, vss, vsh, Hkv, Skv, vchunks, V_AMAX_ROWS, vpart, blk);
+    vamax_rows<D, DT, true>(v, vsb, vss, vsh, Hkv, Skv, vchunks, vamax_chunk_rows(Skv), vpart, blk);
   else if (blk < nv + nk)
     quant_k_rows64<D, DT>(k, ksb, kss, ksh, Hkv, Skv, Skp, k8, ks, blk - nv);
   else
@@ -518,7 +546,7 @@ static void launch_forward_quant(const void* q, int64_t qsb, int64_t qss, int64_
                                  int8_t* k8, float* ks, uint8_t* v8t, float* vs, hipStream_t st) {
   const int tiles = (Sq + 63) / 64;
   const int Skp = kv_pad(Skv);
-  const int vchunks = (Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS;
+  const int vchunks = vamax_chunks(Skv);
   const int nv = vchunks * B * Hkv;
   const int nk = Skp / 64 * B * Hkv;
   hipLaunchKernelGGL((quant_qk_vamax_kernel<D, DT>), dim3(nv + nk + tiles * B * H), dim3(256), 0, st,
@@ -594,7 +622,7 @@ int quant_kv_impl(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const vo
 }
 
 int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D) {
-  return (int64_t)B * Hkv * ((Skv + V_AMAX_ROWS - 1) / V_AMAX_ROWS) * layout_dim(D) * (int64_t)sizeof(float);
+  return (int64_t)B * Hkv * vamax_chunks(Skv) * layout_dim(D) * (int64_t)sizeof(float);
 }
 
 // Validation of every argument is done by the caller (sage_forward) through the per-stage checks below.
