@@ -11,12 +11,15 @@ Prints ONE JSON line on stdout:
   cpu_baseline the reference's quantized math (the numpy port in oracle/) timed on this host on a head sample
 Everything else (per-kernel times, quantizer GB/s, torch SDPA bf16 on the same GPU) goes to the "detail" object.
 
-usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--config 2]
+usage: python bench.py [--gpus 1] [--steps 100] [--warmup W] [--no-cpu-baseline] [--config 2]
+(default W: at least 20 steps and 0.3 s, enough for the GPU clock to leave its idle state: the first ~25 ms of calls
+run ~15% slower)
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -114,7 +117,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps before the timed ones (default: at least 20 and at least 0.3 s of steps, so "
+                         "that the GPU clock has left its idle state)")
     ap.add_argument("--config", default="2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=50)
@@ -158,6 +163,13 @@ def main():
         # below the router's minimum size sageattn uses SDPA, as the reference does: time the kernel-forced entry
         def step():
             return cdna4_sage.attention(q, k, v, "HND", is_causal=cfg.causal)
+    if args.warmup is None:
+        step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        args.warmup = max(20, math.ceil(0.3 / max(time.perf_counter() - t0, 1e-6)))
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
