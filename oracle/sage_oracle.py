@@ -35,6 +35,11 @@ What each function restates (paths relative to the reference checkout):
                         Bottom-right causal for any q_len / kv_len: query i sees keys j <= i + kv_len - q_len; a
                         query that sees no key (q_len > kv_len) gives a 0 row (the gfx950 convention; the reference
                         sends such calls to SDPA, so this case has no reference value).
+                        ``attn_mask`` (bool, True = attend, broadcastable to [B, H, Sq, Skv]) masks scores to
+                        -inf like the causal mask.  The reference sends every masked call to torch SDPA
+                        (src/rdna4_sage/__init__.py:78-79); the quantized masked math here is this build's own
+                        definition, pinned by the all-True, causal-equivalent and padding-equivalent identities
+                        in tests/test_oracle.py and by the float64 masked softmax ``sdpa_reference``.
 * ``sage_forward_varlen`` src/sageattention/core.py:66-89 (`sageattn_varlen`): one ``sage_forward`` per sequence
                         of the packed batch.
 * ``lse_reference``     src/sageattention/core.py:36-57 (`_lse`).
@@ -244,7 +249,7 @@ def logit_scale_base(d: int) -> np.float32:
 
 def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n: int = 32,
               out_dtype: str = "bf16", threshold: float = RESCALE_THRESHOLD, return_stats: bool = False,
-              kv_split=None):
+              kv_split=None, attn_mask=None):
     """Quantized attention as the reference kernel computes it.
 
     q8 [B, H, Sq, D] int8, qs [B, H, Sq] f32, k8 [B, Hkv, Sp, D] int8, ks [B, Hkv, Sp/32] f32,
@@ -255,7 +260,12 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     counterpart in the reference): for those rows the key tiles run as ``chunks`` contiguous ranges (range c =
     tiles [c * n // chunks, (c + 1) * n // chunks)), each with its own online softmax from m = -inf, stored as
     (m_c, l_c, fp16(O_c / l_c)) and merged with M = max m_c, W_c = exp2((m_c - M) * cl) * l_c, L = sum W_c,
-    O = sum W_c * fp16(O_c / l_c) (float32, chunk order), then the usual epilogue with L."""
+    O = sum W_c * fp16(O_c / l_c) (float32, chunk order), then the usual epilogue with L.  A range in which a row
+    sees no key (l_c = 0, m_c = -inf) stores 0 and weighs 0.
+
+    ``attn_mask``: bool array broadcastable to [B, H, Sq, seq_kv], True where the query attends the key (the
+    convention of torch SDPA's boolean masks; no counterpart in the reference's kernel, which sends masked calls to
+    SDPA).  Masked scores are -inf like the causal ones, ANDed with the causal mask when both are given."""
     B, H, Sq, D = q8.shape
     Hkv = k8.shape[1]
     assert block_n % KV_BLOCK == 0 and H % Hkv == 0
@@ -263,21 +273,27 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     hk = np.arange(H) // grp
     cl = (logit_scale_base(D) * qs.astype(F32)).astype(F32)      # [B, H, Sq]
     n_tiles = (seq_kv + block_n - 1) // block_n
-    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles)
+    if attn_mask is not None:
+        attn_mask = np.broadcast_to(np.asarray(attn_mask, dtype=bool), (B, H, q8.shape[2], seq_kv))
+    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask)
     if kv_split is not None:
         chunks, rows = kv_split
         parts = [_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold,
-                                 c * n_tiles // chunks, (c + 1) * n_tiles // chunks) for c in range(chunks)]
+                                 c * n_tiles // chunks, (c + 1) * n_tiles // chunks, attn_mask)
+                 for c in range(chunks)]
         mm = parts[0][1]
         for _, mc, _ in parts[1:]:
             mm = np.maximum(mm, mc)
         ll = np.zeros_like(l)
         oo = np.zeros_like(o)
         for oc, mc, lc in parts:
-            # each chunk's O is stored normalised by its own l, in fp16 (round to nearest even)
-            rl = (F32(1.0) / lc).astype(F32)
-            pn = (oc * rl[..., None]).astype(F32).astype(np.float16).astype(F32)
-            w = (np.exp2(((mc - mm).astype(F32) * cl).astype(F32)).astype(F32) * lc).astype(F32)
+            # each chunk's O is stored normalised by its own l, in fp16 (round to nearest even); a chunk without
+            # a visible key (l = 0) stores 0 and weighs 0
+            with np.errstate(divide="ignore", invalid="ignore"):
+                rl = np.where(lc > 0, (F32(1.0) / lc).astype(F32), F32(0.0)).astype(F32)
+                pn = (oc * rl[..., None]).astype(F32).astype(np.float16).astype(F32)
+                w = np.where(lc > 0, (np.exp2(((mc - mm).astype(F32) * cl).astype(F32)).astype(F32) * lc).astype(F32),
+                             F32(0.0)).astype(F32)
             ll = (ll + w).astype(F32)
             oo = (oo + (w[..., None] * pn).astype(F32)).astype(F32)
         o = np.where(rows[..., None], oo, o)
@@ -292,8 +308,9 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     return out
 
 
-def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi):
-    """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row."""
+def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi, attn_mask=None):
+    """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row.  attn_mask:
+    None or bool [B, H, Sq, seq_kv], True = attend."""
     B, H, Sq, D = q8.shape
     Hkv, Sp = k8.shape[1], k8.shape[2]
     hk = np.arange(H) // (H // Hkv)
@@ -319,6 +336,11 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
         mask = cols[None, :] >= seq_kv
         if causal:
             mask = mask | (cols[None, :] > rows[:, None] + causal_off)
+        if attn_mask is not None:
+            am = np.zeros((B, H, Sq, block_n), dtype=bool)
+            nv = max(0, min(j0 + block_n, seq_kv) - j0)
+            am[..., :nv] = attn_mask[..., j0:j0 + nv]
+            mask = mask | ~am
         s = np.where(mask, F32(-np.inf), s).astype(F32)
         kst = np.ones((B, Hkv, nsub), dtype=F32)
         nb = min(nsub, ks.shape[2] - j0 // KV_BLOCK)
@@ -374,11 +396,12 @@ def round_output(x: np.ndarray, out_dtype: str) -> np.ndarray:
     return x.astype(F32)
 
 
-def sage_forward(q, k, v, causal=False, sm_scale=None, block_n=32, out_dtype="bf16"):
+def sage_forward(q, k, v, causal=False, sm_scale=None, block_n=32, out_dtype="bf16", attn_mask=None, kv_split=None):
     """Full quantized path on HND float32 arrays holding bf16 / fp16 values: quant_q, quant_kv, attention."""
     q8, qs = quant_q(q, sm_scale)
     k8, ks, v8, vs = quant_kv(k, v)
-    return attention(q8, qs, k8, ks, v8, vs, k.shape[2], causal=causal, block_n=block_n, out_dtype=out_dtype)
+    return attention(q8, qs, k8, ks, v8, vs, k.shape[2], causal=causal, block_n=block_n, out_dtype=out_dtype,
+                     attn_mask=attn_mask, kv_split=kv_split)
 
 
 def sage_forward_varlen(q, k, v, cu_q, cu_k, causal=False, sm_scale=None, block_n=64, out_dtype="bf16"):
@@ -405,8 +428,9 @@ def sage_forward_varlen(q, k, v, cu_q, cu_k, causal=False, sm_scale=None, block_
 # ----------------------------------------------------------------------------------------------------------
 # Textbook references used to bound the emulation
 # ----------------------------------------------------------------------------------------------------------
-def sdpa_reference(q, k, v, causal=False, sm_scale=None):
-    """float64 softmax attention, bottom-right causal, GQA by head repetition."""
+def sdpa_reference(q, k, v, causal=False, sm_scale=None, attn_mask=None):
+    """float64 softmax attention, bottom-right causal, GQA by head repetition; attn_mask: bool, broadcastable to
+    [B, H, Sq, Skv], True = attend.  A row that sees no key is 0."""
     B, H, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
     rep = H // Hkv
@@ -417,9 +441,13 @@ def sdpa_reference(q, k, v, causal=False, sm_scale=None):
     if causal:
         mask = np.arange(Skv)[None, :] > np.arange(Sq)[:, None] + (Skv - Sq)
         s = np.where(mask, -np.inf, s)
-    s = s - s.max(axis=-1, keepdims=True)
-    p = np.exp(s)
-    p /= p.sum(axis=-1, keepdims=True)
+    if attn_mask is not None:
+        s = np.where(np.broadcast_to(np.asarray(attn_mask, dtype=bool), s.shape), s, -np.inf)
+    mx = s.max(axis=-1, keepdims=True)
+    seen = np.isfinite(mx)
+    p = np.exp(s - np.where(seen, mx, 0.0))
+    den = p.sum(axis=-1, keepdims=True)
+    p = np.where(seen, p / np.where(seen, den, 1.0), 0.0)
     return np.matmul(p, vv)
 
 

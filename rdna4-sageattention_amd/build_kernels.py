@@ -25,7 +25,7 @@ INCLUDE = ROOT.parent / "include"
 LIB = PKG / "libsage_capi.so"
 MANIFEST = PKG / "manifest.json"
 ARCH = "gfx950"
-SOURCES = ("sage_capi.hip", "sage_quant.hip", "sage_attn.hip", "sage_lse.hip", "sage_varlen.hip")
+SOURCES = ("sage_capi.hip", "sage_quant.hip", "sage_attn.hip", "sage_lse.hip", "sage_varlen.hip", "sage_mask.hip")
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -6,10 +6,11 @@ libsage_capi.so and launched through its C ABI on torch's current stream.
     import cdna4_sage
     out = cdna4_sage.sageattn(q, k, v, tensor_layout="HND")   # drop-in for sageattention.sageattn
 
-Routing mirrors the reference's src/rdna4_sage/__init__.py:20-84: masks, small problems, unsupported shapes or GPUs
-and causal calls with q_len > kv_len go to torch's SDPA binding; everything else runs the gfx950 kernels (causal
-calls with q_len < kv_len too, bottom-right aligned, where the reference uses SDPA).  attention_varlen runs packed
-variable-length batches in one pass.
+Routing mirrors the reference's src/rdna4_sage/__init__.py:20-84: small problems, unsupported shapes or GPUs,
+float (additive) masks and causal calls with q_len > kv_len go to torch's SDPA binding; everything else runs the
+gfx950 kernels, including two cases the reference sends to SDPA: causal calls with q_len < kv_len (bottom-right
+aligned) and boolean attn_masks (set CDNA4_SAGE_NATIVE_MASK=0 to send masks to SDPA as the reference does).
+attention_varlen runs packed variable-length batches in one pass.
 """
 import os
 
@@ -17,7 +18,8 @@ import torch
 from torch.nn.attention.bias import causal_lower_right
 
 from . import ops
-from ._attention import ARCHS, HEAD_DIMS, Unsupported, attention_varlen, check_supported, device_arch, lse
+from ._attention import (ARCHS, HEAD_DIMS, Unsupported, attention_varlen, check_supported, device_arch, lse,
+                         mask_view)
 
 __all__ = ["sageattn", "attention", "attention_varlen", "lse", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
 __version__ = "0.1.0"
@@ -38,6 +40,8 @@ def _env_int(names, default):
 # CDNA4_SAGE_* take precedence; the reference's RDNA4_SAGE_* names are honoured for drop-in callers.
 MIN_WORK = _env_int(("CDNA4_SAGE_MIN_WORK", "RDNA4_SAGE_MIN_WORK"), 64 * 2**20)  # batch * heads * q_len * kv_len
 MIN_KV = _env_int(("CDNA4_SAGE_MIN_KV", "RDNA4_SAGE_MIN_KV"), 1024)
+# Boolean attn_masks run on the kernel (quantized like every other call); 0 restores the reference's SDPA routing.
+NATIVE_MASK = _env_int(("CDNA4_SAGE_NATIVE_MASK",), 1) != 0
 
 
 def is_available(device=None) -> bool:
@@ -48,10 +52,14 @@ def is_available(device=None) -> bool:
     return device_arch(dev) in ARCHS
 
 
-def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False):
+def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False, attn_mask=None):
     """Run the int8/fp8 kernel; raises Unsupported if it cannot.  Output in the input layout and dtype.
-    Causal attention is bottom-right aligned and needs q_len <= kv_len."""
-    out = ops.attention(q, k, v, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
+    Causal attention is bottom-right aligned and needs q_len <= kv_len.  attn_mask: None or a boolean mask (True =
+    attend) broadcastable to [B, H, q_len, kv_len]; a query row that sees no key is 0."""
+    if attn_mask is None:
+        out = ops.attention(q, k, v, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
+    else:
+        out = ops.attention_masked(q, k, v, attn_mask, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
     return out.transpose(1, 2) if tensor_layout == "HND" else out
 
 
@@ -86,14 +94,17 @@ def _worth_it(q, k, tensor_layout, is_causal=False):
 
 def sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, attn_mask=None, return_lse=False, **kwargs):
     """Drop-in for sageattention.sageattn.  Uses the gfx950 kernel when it applies and pays off, torch SDPA otherwise
-    (masks, causal with q_len > kv_len, unsupported shapes or GPUs, small problems).  Causal attention is
-    bottom-right aligned as in SageAttention / FlashAttention.  Extra SageAttention kwargs are ignored."""
+    (float masks, causal with q_len > kv_len, unsupported shapes or GPUs, small problems).  Causal attention is
+    bottom-right aligned as in SageAttention / FlashAttention.  A boolean attn_mask runs on the kernel (a query row
+    that sees no key gives 0 there, NaN in SDPA).  Extra SageAttention kwargs are ignored."""
     if return_lse:
         raise NotImplementedError("cdna4_sage: return_lse is not supported here; use sageattention.sageattn")
-    if attn_mask is not None or not _worth_it(q, k, tensor_layout, is_causal):
+    if (attn_mask is not None and not NATIVE_MASK) or not _worth_it(q, k, tensor_layout, is_causal):
         return _sdpa(q, k, v, tensor_layout, is_causal, sm_scale, attn_mask)
     try:
         check_supported(q, k, v, tensor_layout, is_causal)
+        if attn_mask is not None:
+            mask_view(attn_mask, q, k, tensor_layout)
     except Unsupported:
         return _sdpa(q, k, v, tensor_layout, is_causal, sm_scale, attn_mask)
-    return attention(q, k, v, tensor_layout, sm_scale, is_causal)
+    return attention(q, k, v, tensor_layout, sm_scale, is_causal, attn_mask=attn_mask)

@@ -88,10 +88,42 @@ def _ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
-def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
-    """Attention without mask, optionally causal (bottom-right aligned, q_len <= kv_len).  q: (B, H, Sq, D) for "HND" or (B, Sq, H, D) for
-    "NHD"; k/v alike, with H a multiple of the kv head count.  Returns (B, Sq, H, D) contiguous in q's dtype."""
+def _shape(q, k, layout):
+    if layout == "HND":
+        return q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3]
+    return q.shape[0], q.shape[2], k.shape[2], q.shape[1], k.shape[1], q.shape[3]
+
+
+def mask_view(attn_mask, q, k, layout):
+    """A boolean attn_mask (True = attend, broadcastable to [B, H, q_len, kv_len] as torch SDPA's) as the kernel reads
+    it: the mask expanded to [B, H, q_len, kv_len] with the key axis contiguous and broadcast axes at stride 0, and
+    its (batch, head, row) byte strides.  Only the key axis is ever materialised.  Raises Unsupported for float
+    masks (additive biases stay on SDPA) and for masks that do not broadcast."""
+    if not isinstance(attn_mask, torch.Tensor) or attn_mask.dtype != torch.bool:
+        raise Unsupported("only boolean attn_mask runs on the kernel (additive float masks go to SDPA)")
+    if attn_mask.device != q.device:
+        raise Unsupported("attn_mask must be on the device of q")
+    if attn_mask.dim() > 4:
+        raise Unsupported(f"attn_mask with {attn_mask.dim()} dims")
+    B, H, _, Sq, Skv, _ = _shape(q, k, layout)
+    try:
+        m = attn_mask.expand(B, H, Sq, Skv)
+    except RuntimeError as e:
+        raise Unsupported(f"attn_mask of shape {tuple(attn_mask.shape)} does not broadcast to {(B, H, Sq, Skv)}") from e
+    if Skv > 1 and m.stride(3) != 1:
+        base = attn_mask.reshape((1,) * (4 - attn_mask.dim()) + tuple(attn_mask.shape))
+        m = base.expand(*base.shape[:3], Skv).contiguous().expand(B, H, Sq, Skv)
+    return m, (m.stride(0), m.stride(1), m.stride(2))
+
+
+def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False, attn_mask=None):
+    """Attention, optionally causal (bottom-right aligned, q_len <= kv_len) and / or with a boolean attn_mask (True =
+    attend, broadcastable to [B, H, q_len, kv_len]; ANDed with the causal mask; a query row that sees no key is 0).
+    q: (B, H, Sq, D) for "HND" or (B, Sq, H, D) for "NHD"; k/v alike, with H a multiple of the kv head count.
+    Returns (B, Sq, H, D) contiguous in q's dtype."""
     check_supported(q, k, v, layout, is_causal)
+    if attn_mask is not None:
+        mask, mstr = mask_view(attn_mask, q, k, layout)
     dev = q.device
     if layout == "HND":
         B, H, Sq, D = q.shape
@@ -114,8 +146,17 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False):
     v8t = torch.empty((B, Hkv, dl, skp), device=dev, dtype=torch.uint8)
     vs = torch.empty((B, Hkv, dl), device=dev, dtype=torch.float32)
     out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
-    ws_bytes = _capi.forward_workspace(dev.index if dev.index is not None else torch.cuda.current_device(),
-                                       B, H, Hkv, Sq, Skv, D, bool(is_causal))
+    di = dev.index if dev.index is not None else torch.cuda.current_device()
+    if attn_mask is not None:
+        ws_bytes = _capi.mask_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal), *mstr)
+        ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+        with torch.cuda.device(dev):
+            _capi.call("sage_forward_masked", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out),
+                       *_out_strides(out), B, H, Hkv, Sq, Skv, D, dt, int(bool(is_causal)),
+                       qs_fold_factor(sm_scale, D), _ptr(mask), *mstr, _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks),
+                       _ptr(v8t), _ptr(vs), _ptr(ws), ws_bytes, stream)
+        return out
+    ws_bytes = _capi.forward_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal))
     ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         _capi.call("sage_forward", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),

@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsage_capi.so"
 
 SAGE_OK, SAGE_ERR_INVALID, SAGE_ERR_UNSUPPORTED, SAGE_ERR_HIP = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F16 = 0, 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()
@@ -47,6 +47,10 @@ SIGNATURES = {
     "sage_varlen_layout": ([_I, _I, _I, _I, _I, _P, _P], _I),
     "sage_forward_varlen": ([_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _P,
                              _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
+    "sage_mask_workspace": ([_I, _I, _I, _I, _I, _I, _I, _L, _L, _L, _P], _I),
+    "sage_forward_masked": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
+                             _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _L, _L,
+                             _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
 }
 
 
@@ -109,6 +113,16 @@ def forward_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv:
     ws = ctypes.c_int64()
     with torch.cuda.device(device_index):
         call("sage_forward_workspace", B, H, Hkv, Sq, Skv, D, int(causal), ctypes.byref(ws))
+    return ws.value
+
+
+@functools.lru_cache(maxsize=4096)
+def mask_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv: int, D: int, causal: bool, msb: int,
+                   msh: int, msq: int) -> int:
+    """Workspace bytes of sage_forward_masked for this shape and mask strides on device `device_index`."""
+    ws = ctypes.c_int64()
+    with torch.cuda.device(device_index):
+        call("sage_mask_workspace", B, H, Hkv, Sq, Skv, D, int(causal), msb, msh, msq, ctypes.byref(ws))
     return ws.value
 
 

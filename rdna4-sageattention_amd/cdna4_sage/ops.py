@@ -1,4 +1,4 @@
-"""torch.library registration: torch.ops.cdna4_sage.attention, traceable by torch.compile.
+"""torch.library registration: torch.ops.cdna4_sage.attention (and attention_masked), traceable by torch.compile.
 
 Same schema as the reference's rdna4_sage::attention (src/rdna4_sage/ops.py:7-17); the rdna4_sage package of this
 repo registers that name too, for callers that use it directly.
@@ -25,3 +25,16 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: str, sm
 
 
 attention.register_fake(_fake)
+
+
+@torch.library.custom_op("cdna4_sage::attention_masked", mutates_args=())
+def attention_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn_mask: torch.Tensor, layout: str,
+                     sm_scale: float, is_causal: bool) -> torch.Tensor:
+    """attention with a boolean attn_mask (True = attend, broadcastable to [B, H, q_len, kv_len]); no counterpart in
+    the reference, which sends masked calls to SDPA.  Returns (B, Sq, H, D) contiguous."""
+    return _attention.attention(q, k, v, layout, sm_scale if sm_scale > 0 else None, is_causal, attn_mask=attn_mask)
+
+
+@attention_masked.register_fake
+def _fake_masked(q, k, v, attn_mask, layout, sm_scale, is_causal):
+    return _fake(q, k, v, layout, sm_scale, is_causal)

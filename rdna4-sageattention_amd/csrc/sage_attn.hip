@@ -70,15 +70,18 @@ struct VarlenTiles {
   const int* kp;      // [batch + 1] padded key offsets
 };
 
+
 // D is the channel count of the Q8 / K8 / V8T layouts; `dout` output channels are written (96 for head_dim 96, whose
 // layouts are zero-padded to 128; D otherwise).  c0 = log2(e) / sqrt(head_dim).
-template <int D, bool CAUSAL, int OUT_DT, bool VARLEN>
+// MASK: a boolean mask (MaskTabs) instead of the causal / padding bound; the causal flag is folded into its bits.
+template <int D, bool CAUSAL, int OUT_DT, bool VARLEN, bool MASK = false>
 __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ qs, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
     int Sq_arg, int Skv_arg, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part,
-    float c0, int dout, VarlenTiles vt) {
+    float c0, int dout, VarlenTiles vt, MaskTabs mt) {
+  static_assert(!(MASK && (CAUSAL || VARLEN)), "the mask variant folds causality into its bits and is dense only");
   constexpr int BN = ATT_BN;
   constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
   constexpr int VTILE = D * BN;      // bytes of the V tile  ([D channels][64 keys])
@@ -160,6 +163,37 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     t_hi = (ch + 1) * ntiles / chunks;
   }
 
+  // ---- mask: this lane's bit row and this wave's class row; the workgroup skips the tiles before the first and
+  // after the last tile that any of its rows sees (the skipped tiles hold no visible key, so skipping them is
+  // exactly the online softmax over them) ----
+  const uint8_t* mbase = nullptr;  // this (batch, head)'s mask words; the lane's row at byte offset moff
+  uint32_t moff = 0;                 // (the bits array is below 2 GiB, checked on the host)
+  const int* mcls = nullptr;
+  if (MASK) {
+    mbase = reinterpret_cast<const uint8_t*>(mt.bits + (int64_t)b * mt.bsb + (int64_t)h * mt.bsh);
+    moff = (uint32_t)(((int64_t)qr * mt.bsq + hf) * 4);
+    mcls = mt.cls + (int64_t)b * mt.csb + (int64_t)h * mt.csh + (int64_t)min(q0 >> 5, mt.groups - 1) * mt.csg;
+    __shared__ int mrange[2];
+    if (threadIdx.x == 0) {
+      mrange[0] = ntiles;
+      mrange[1] = -1;
+    }
+    __syncthreads();
+    int lo = ntiles, hi = -1;
+    for (int t = lane; t < ntiles; t += 64)
+      if (mcls[t] != 0) {
+        lo = min(lo, t);
+        hi = max(hi, t);
+      }
+    if (hi >= 0) {
+      atomicMin(&mrange[0], lo);
+      atomicMax(&mrange[1], hi);
+    }
+    __syncthreads();
+    t_lo = max(t_lo, mrange[0]);
+    t_hi = min(t_hi, mrange[1] + 1);
+  }
+
   const int8_t* kbase = k8 + ((int64_t)khead * Skp + kofs) * D;
   const uint8_t* vbase = v8t + (int64_t)khead * D * Skp + kofs;
   const float* ksb = ks + ((int64_t)khead * Skp + kofs) / SAGE_KV_BLOCK;
@@ -216,7 +250,9 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
   v8i pb = {};  // E4M3 probabilities (B operand of the PV MFMA); each cvt rewrites one half, so no clearing
 
   // One tile: S^T = K Q^T (int8 MFMA), online softmax with the reference's lazy rescale, O^T += V^T P^T (fp8 MFMA).
-#define SAGE_TILE(T, MASKED)                                                                               \
+  // MODE 0: every key visible; 1: keys beyond the causal / padding bound masked; 2: keys whose bit of MW is clear
+  // masked (MW = the lane's mask word of the tile).
+#define SAGE_TILE(T, MODE, MW)                                                                             \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
     const uint8_t* kt_ = smem[t_ & 1];                                                                     \
@@ -231,13 +267,21 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     float sf_[2][16];                                                                                      \
     _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] = __int_as_float(s_[kb_][v_]);        \
-    if (MASKED) {                                                                                          \
+    if ((MODE) == 1) {                                                                                     \
       /* element (kb, v) holds key t * 64 + 4 hf + c with the constant c = 32 kb + 8 (v / 4) + v % 4; it is    \
          visible iff key <= min(Skv - 1, qr + off), i.e. c <= lim (one 32-bit bound per tile and lane) */   \
       const int lim_ = (CAUSAL ? min(Skv - 1, qr + off) : Skv - 1) - (t_ * BN + 4 * hf);                   \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
           if (32 * kb_ + 8 * (v_ >> 2) + (v_ & 3) > lim_) sf_[kb_][v_] = -INFINITY;                        \
+        }                                                                                                  \
+    }                                                                                                      \
+    if ((MODE) == 2) {                                                                                     \
+      /* keep = all ones where bit 16 kb + v of the word is set: one extract and one bit select per score */ \
+      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
+          const int keep_ = __builtin_amdgcn_sbfe((int)(MW), 16 * kb_ + v_, 1);                            \
+          sf_[kb_][v_] = __int_as_float((__float_as_int(sf_[kb_][v_]) & keep_) | (int)(0xFF800000u & ~(uint32_t)keep_)); \
         }                                                                                                  \
     }                                                                                                      \
     float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                              \
@@ -254,7 +298,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     const float mnew_ = need_ ? mcand_ : m;                                                                \
     /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets    \
        from 0 instead of -inf keep corr and the exponents free of NaN */                                   \
-    const float mref_ = (MASKED && mnew_ == -INFINITY) ? 0.0f : mnew_;                                     \
+    const float mref_ = ((MODE) != 0 && mnew_ == -INFINITY) ? 0.0f : mnew_;                               \
     const float corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                          \
     const float neg_ = 0.0f - cl * mref_;                                                                  \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
@@ -302,17 +346,51 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   int t = t_lo;
-  for (; t < t_mask; ++t) {
-    if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
-    SAGE_TILE(t, false);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
-  for (; t < t_hi; ++t) {
-    if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
-    SAGE_TILE(t, true);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  if (MASK) {
+    // per wave and tile: skip (class 0), the mask-free body (1) or the bit-masked body (2).  Runs of tiles of
+    // classes 0 / 1 and runs of class 2 go through two loops with one tile body each (one loop holding both bodies
+    // spills); each iteration of either ends in the workgroup barrier of its tile, and s_barrier counts waves, not
+    // program locations, so the waves of a workgroup may sit in different loops.  The class of the next tile is
+    // loaded one iteration ahead (scalar); the lane's mask word is loaded before the next tile's direct loads are
+    // issued, so the wait for it (after the QK MFMAs) does not wait for the tile data.
+    int c_nxt = t < t_hi ? mcls[t] : 0;
+    while (t < t_hi) {
+      for (; t < t_hi && c_nxt != 2; ++t) {
+        const int c_cur = c_nxt;
+        if (t + 1 < t_hi) {
+          c_nxt = mcls[t + 1];
+          SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+        }
+        if (c_cur == 1) SAGE_TILE(t, 0, 0u);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
+      for (; t < t_hi && c_nxt == 2; ++t) {
+        const uint8_t* mb_ = mbase;
+        asm volatile("" : "+s"(mb_));
+        const uint32_t mw_ = *reinterpret_cast<const uint32_t*>(mb_ + (moff + 8u * (uint32_t)t));
+        if (t + 1 < t_hi) {
+          c_nxt = mcls[t + 1];
+          SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+        }
+        SAGE_TILE(t, 2, mw_);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
+    }
+  } else {
+    for (; t < t_mask; ++t) {
+      if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+      SAGE_TILE(t, 0, 0u);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+    for (; t < t_hi; ++t) {
+      if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+      SAGE_TILE(t, 1, 0u);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
   }
 #undef SAGE_ISSUE_TILE
 #undef SAGE_TILE
@@ -322,7 +400,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
   if (split) {
     // partial state of this key range (workspace layout at ws_ml_offset), merged by attn_merge_kernel
     const int q = wave * 32 + ln;
-    const float rl = 1.0f / lt;
+    const float rl = lt > 0.0f ? 1.0f / lt : 0.0f;  // a range in which the row sees no key stores 0
     uint16_t* po = reinterpret_cast<uint16_t*>(part) + ((int64_t)unit * ATT_BM + q) * D;
 #pragma unroll
     for (int i = 0; i < NPV; ++i)
@@ -411,7 +489,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 #pragma unroll
   for (int i = 0; i < ATT_MAX_CHUNKS; ++i) {
     if (i < chunks) {
-      const float w = __builtin_amdgcn_exp2f((e[i].x - M) * cl) * e[i].y;  // chunk weight times its l
+      // chunk weight times its l; a range in which the row sees no key (l = 0, m = -inf) weighs 0
+      const float w = e[i].y > 0.0f ? __builtin_amdgcn_exp2f((e[i].x - M) * cl) * e[i].y : 0.0f;
       L = L + w;
       acc.x = acc.x + w * f16_lo(oi[i].x);
       acc.y = acc.y + w * f16_hi(oi[i].x);
@@ -419,7 +498,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
       acc.w = acc.w + w * f16_hi(oi[i].y);
     }
   }
-  const float inv = (1.0f / 448.0f) / L;
+  const float inv = L > 0.0f ? (1.0f / 448.0f) / L : 0.0f;  // a row without any visible key is written as 0
   const v4f sc4 = *reinterpret_cast<const v4f*>(vs + (int64_t)bhk * D + 4 * cg);
   const uint32_t e0 = f32_to_out_bits<OUT_DT>((acc.x * inv) * sc4[0]);
   const uint32_t e1 = f32_to_out_bits<OUT_DT>((acc.y * inv) * sc4[1]);
@@ -523,7 +602,7 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
                      vs, o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks,
-                     part, c0, hd, VarlenTiles{});
+                     part, c0, hd, VarlenTiles{}, MaskTabs{});
   if (n_split > 0) {
     if ((rc = check_launch("attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
@@ -591,7 +670,7 @@ static int launch_attn_varlen(const int8_t* q8, const float* qs, const int8_t* k
                               int TQ, int TKP, int hd, int n_blocks, VarlenTiles vt, hipStream_t st) {
   hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
                      v8t, vs, static_cast<uint16_t*>(out), (int64_t)0, oss, osh, nullptr, H, Hkv, TQ, 0, TKP, 0,
-                     n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt);
+                     n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt, MaskTabs{});
   return check_launch("varlen attention launch");
 }
 
@@ -603,6 +682,55 @@ int attn_varlen_impl(const int8_t* q8, const float* qs, const int8_t* k8, const 
   const VarlenTiles vt{static_cast<const int4*>(tiles), cu_q, cu_k, kp};
   return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn_varlen, q8, qs, k8, ks, v8t, vs, out,
                             oss, osh, H, Hkv, TQ, TKP, D, n_blocks, vt, (hipStream_t)stream);
+}
+
+// Masked attention (the mask variant of the kernel; validation by the caller, sage_forward_masked).  The plan is
+// the dense non-causal one (sage_attn_plan with causal = 0; the causal flag lives in the mask bits), so callers can
+// query it; the mask variant's occupancy is never below the dense kernel's.
+template <int D, bool CAUSAL, int OUT_DT>
+static int plan_mask(int B, int H, int Sq, int Skv, AttnPlan* p) {
+  return make_plan<D, false, OUT_DT>(B, H, Sq, Skv, p);
+}
+
+int attn_mask_plan_impl(int B, int H, int Sq, int Skv, int D, int64_t* ws) {
+  AttnPlan p;
+  int rc = SAGE_ATTN_DISPATCH(D, false, true, plan_mask, B, H, Sq, Skv, &p);
+  if (rc) return rc;
+  *ws = p.workspace;
+  return SAGE_OK;
+}
+
+template <int D, bool CAUSAL, int OUT_DT>
+static int launch_attn_mask(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
+                            const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv,
+                            int Sq, int Skv, int hd, MaskTabs mt, void* workspace, hipStream_t st) {
+  AttnPlan p;
+  int rc;
+  if ((rc = plan_mask<D, false, OUT_DT>(B, H, Sq, Skv, &p))) return rc;
+  const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
+  const int n_split = p.n_tiles - p.n_full;
+  const int blocks = p.n_full + n_split * p.chunks;
+  const float c0 = logit_scale_base(hd);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  float* part = static_cast<float*>(workspace);
+  hipLaunchKernelGGL((attn_kernel<D, false, OUT_DT, false, true>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8,
+                     ks, v8t, vs, o, osb, oss, osh, nullptr, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles,
+                     p.n_full, p.chunks, part, c0, hd, VarlenTiles{}, mt);
+  if (n_split > 0) {
+    if ((rc = check_launch("masked attention launch"))) return rc;
+    hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
+                       part, qs, vs, o, osb, oss, osh, nullptr, H, Hkv, Sq, q_tiles, p.n_full, n_split, p.chunks, c0,
+                       hd);
+  }
+  return check_launch("masked attention launch");
+}
+
+// workspace: at least attn_mask_plan_impl bytes (may be NULL when that is 0)
+int attn_mask_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
+                   const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq,
+                   int Skv, int D, int out_dtype, const MaskTabs* mt, void* workspace, void* stream) {
+  return SAGE_ATTN_DISPATCH(D, false, out_dtype == SAGE_DTYPE_BF16, launch_attn_mask, q8, qs, k8, ks, v8t, vs, out,
+                            osb, oss, osh, B, H, Hkv, Sq, Skv, D, *mt, workspace, (hipStream_t)stream);
 }
 
 }  // namespace sage

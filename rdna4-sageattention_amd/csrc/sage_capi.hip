@@ -48,7 +48,7 @@ static int forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int 
 
 extern "C" {
 
-int sage_abi_version(void) { return 3; }
+int sage_abi_version(void) { return 4; }
 
 const char* sage_last_error(void) { return sage::g_err; }
 

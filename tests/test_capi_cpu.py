@@ -151,3 +151,34 @@ def test_varlen_validates_before_launching():
     assert call(ws_bytes=ws_bytes - 1) == _capi.SAGE_ERR_INVALID and "workspace" in _err()
     assert call(ws=P + 16) == _capi.SAGE_ERR_INVALID and "256-byte" in _err()
     assert call(total_q=0) == _capi.SAGE_ERR_INVALID
+
+
+def test_masked_forward_validates_before_launching():
+    """sage_forward_masked / sage_mask_workspace reject bad shapes, strides and pointers with a code and a message
+    before the first HIP call (on this GPU-less machine any later step would fail with a HIP error instead)."""
+    lib = _capi.lib()
+    args = dict(q=P, qsb=0, qss=128, qsh=0, k=P, ksb=0, kss=128, ksh=0, v=P, vsb=0, vss=128, vsh=0, out=P, osb=0,
+                oss=128, osh=128, B=1, H=4, Hkv=2, Sq=80, Skv=200, D=128, dtype=0, causal=0, qs_mul=1.0,
+                mask=P, msb=0, msh=0, msq=200, q8=P, qs=P, k8=P, ks=P, v8t=P, vs=P, ws=P, ws_bytes=1 << 30,
+                stream=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.sage_forward_masked(*a.values())
+
+    assert call(D=80) == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 80" in _err()
+    assert call(causal=1, Sq=300) == _capi.SAGE_ERR_UNSUPPORTED and "causal" in _err()
+    assert call(Hkv=3) == _capi.SAGE_ERR_INVALID and "multiple" in _err()
+    assert call(msq=-1) == _capi.SAGE_ERR_INVALID and "mask strides" in _err()
+    assert call(dtype=5) == _capi.SAGE_ERR_UNSUPPORTED
+    assert call(mask=None) == _capi.SAGE_ERR_INVALID and "mask is NULL" in _err()
+    assert call(out=P + 8) == _capi.SAGE_ERR_INVALID and "out" in _err()
+    assert call(oss=100) == _capi.SAGE_ERR_INVALID and "multiples of 8" in _err()
+    assert call(ws=None) == _capi.SAGE_ERR_INVALID and "workspace" in _err()
+    assert call(ws=P + 16) == _capi.SAGE_ERR_INVALID and "256-byte" in _err()
+    assert call(Sq=1 << 20, Skv=1 << 30) == _capi.SAGE_ERR_INVALID and "too large" in _err()
+    ws = ctypes.c_int64(-1)
+    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 96, 1, 0, 0, -5, ctypes.byref(ws)) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 80, 0, 0, 0, 0, ctypes.byref(ws)) == _capi.SAGE_ERR_UNSUPPORTED
+    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 128, 0, 0, 0, 0, None) == _capi.SAGE_ERR_INVALID
+    assert ws.value == -1

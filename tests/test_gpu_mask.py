@@ -1,0 +1,174 @@
+"""Boolean attn_mask on the gfx950 kernel (sage_forward_masked) vs the CPU emulation with the same mask and vs the
+float64 masked softmax.
+
+Tolerances as for the unmasked kernel: max |out - emulation| <= 2e-2 (emulation at the kernel's 64-key tile and
+split plan) and cosine >= 0.999 against float attention with the mask.  Identities: an all-True mask gives the
+unmasked kernel's output bit for bit; a mask whose rows see no key gives 0 rows and no NaN elsewhere.  The reference
+sends masked calls to torch SDPA (src/rdna4_sage/__init__.py:78-79); its tests have no masked case.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import cdna4_sage
+from cdna4_sage import _capi
+from gpu_util import cosine, hnd_np, kv_split
+from oracle import sage_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+COS = 0.999
+
+
+def _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Sq, D, generator=g).to(dt)
+    k = torch.randn(B, Hkv, Skv, D, generator=g).to(dt)
+    v = torch.randn(B, Hkv, Skv, D, generator=g).to(dt)
+    if layout == "NHD":
+        q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    return q, k, v
+
+
+def _emulate(q, k, v, layout, causal, mask, split, out_dtype):
+    qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
+    q8, qs = orc.quant_q(qn)
+    k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(kn.shape[2]))
+    m = mask.cpu().numpy()
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=64, out_dtype=out_dtype,
+                        kv_split=split, attn_mask=m)
+    ref = orc.sdpa_reference(qn, kn, vn, causal=causal, attn_mask=m)
+    return emu, ref
+
+
+def _key_padding(B, Skv, lengths):
+    return torch.arange(Skv)[None, None, None, :] < torch.tensor(lengths)[:, None, None, None]
+
+
+def _block_diagonal(S, bounds):
+    seg = torch.zeros(S, dtype=torch.long)
+    for b in bounds:
+        seg[b:] += 1
+    return (seg[:, None] == seg[None, :])[None, None]
+
+
+def _random(shape, p, seed):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.rand(shape, generator=g) < p
+    return m
+
+
+def _cases():
+    c = []
+    # B, H, Hkv, Sq, Skv, D, dtype, layout, causal, mask builder
+    c.append(("key padding", (2, 2, 2, 300, 1031, 128, torch.bfloat16, "HND", False),
+              lambda: _key_padding(2, 1031, [700, 1031])))
+    c.append(("random full", (1, 2, 1, 257, 400, 64, torch.float16, "NHD", False),
+              lambda: _random((1, 2, 257, 400), 0.7, 1)))
+    c.append(("causal + key padding", (1, 2, 2, 500, 500, 128, torch.bfloat16, "HND", True),
+              lambda: _key_padding(1, 500, [450])))
+    c.append(("block diagonal", (1, 2, 2, 1000, 1000, 128, torch.bfloat16, "HND", False),
+              lambda: _block_diagonal(1000, [130, 512, 700])))
+    c.append(("2-D mask, GQA, d256", (2, 4, 2, 200, 333, 256, torch.bfloat16, "NHD", False),
+              lambda: _random((200, 333), 0.5, 2)))
+    c.append(("head_dim 96", (1, 2, 2, 300, 300, 96, torch.float16, "HND", False),
+              lambda: _random((1, 1, 300, 300), 0.8, 3)))
+    c.append(("causal q < kv, random", (1, 3, 3, 130, 777, 64, torch.bfloat16, "HND", True),
+              lambda: _random((1, 3, 130, 777), 0.6, 4)))
+    return c
+
+
+CASES = _cases()
+
+
+@pytest.mark.parametrize("name,shape,make_mask", CASES, ids=[c[0] for c in CASES])
+def test_masked_attention_vs_emulation(dev, name, shape, make_mask):
+    B, H, Hkv, Sq, Skv, D, dt, layout, causal = shape
+    q, k, v = _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=Sq + Skv + D)
+    mask = make_mask()
+    if name == "random full":
+        mask[0, 1, 7] = False           # a row that sees no key
+        mask[0, 0, 9] = False
+        mask[0, 0, 9, 399] = True       # a row that sees one key of the last (partial) tile
+    print(f"case {name}: B={B} H={H} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} {dt} {layout} causal={causal} "
+          f"mask {tuple(mask.shape)}", flush=True)
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), tensor_layout=layout, is_causal=causal,
+                               attn_mask=mask.to(dev))
+    assert out.shape == q.shape and out.dtype == dt
+    got = hnd_np(out, layout)
+    assert np.isfinite(got).all()
+    split = kv_split(dev, B, H, Sq, Skv, D, False)   # the masked call uses the dense non-causal plan
+    full = torch.broadcast_to(mask, (B, H, Sq, Skv))
+    emu, ref = _emulate(q, k, v, layout, causal, full, split, "bf16" if dt == torch.bfloat16 else "f16")
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS, err
+    assert cosine(got, ref) >= COS
+    if name == "random full":
+        assert (got[0, 1, 7] == 0).all() and (ref[0, 1, 7] == 0).all()
+        assert np.abs(got[0, 0, 9] - emu[0, 0, 9]).max() <= MAX_ABS
+
+
+def test_all_true_mask_is_the_unmasked_kernel(dev):
+    """Every tile of an all-True mask takes the mask-free body, the partial last tile the bit-masked one: the output
+    must equal the unmasked call bit for bit (same plan, same arithmetic)."""
+    q, k, v = (t.to(dev) for t in _inputs(1, 4, 2, 700, 1100, 128, torch.bfloat16, "HND", seed=5))
+    base = cdna4_sage.attention(q, k, v)
+    for m in (torch.ones(1100, dtype=torch.bool), torch.ones(1, 4, 700, 1100, dtype=torch.bool)):
+        assert torch.equal(cdna4_sage.attention(q, k, v, attn_mask=m.to(dev)), base)
+
+
+def test_fully_masked_rows_and_tiles_give_zero(dev):
+    q, k, v = (t.to(dev) for t in _inputs(2, 2, 2, 300, 600, 64, torch.float16, "HND", seed=6))
+    none = torch.zeros(2, 1, 1, 600, dtype=torch.bool, device=dev)
+    out = cdna4_sage.attention(q, k, v, attn_mask=none)
+    assert torch.isfinite(out).all() and (out == 0).all()
+    half = torch.ones(2, 2, 300, 600, dtype=torch.bool, device=dev)
+    half[1, :, 128:] = False        # whole query tiles (split or not) without any visible key
+    out = cdna4_sage.attention(q, k, v, attn_mask=half)
+    assert (out[1, :, 128:] == 0).all() and torch.equal(out[0], cdna4_sage.attention(q, k, v)[0])
+
+
+def test_sageattn_routes_bool_masks_to_the_kernel(dev, monkeypatch):
+    """sageattn (and sageattention.sageattn through kwargs) runs boolean masks on the kernel above the routing
+    threshold, float masks on SDPA; CDNA4_SAGE_NATIVE_MASK=0 restores the reference's SDPA routing."""
+    import sageattention
+    monkeypatch.setattr(cdna4_sage, "MIN_WORK", 0)      # 8 x 1024 x 1024 is below the default threshold
+    q, k, v = (t.to(dev) for t in _inputs(1, 8, 8, 1024, 1024, 64, torch.bfloat16, "HND", seed=7))
+    mask = _key_padding(1, 1024, [900]).to(dev)
+    kern = cdna4_sage.attention(q, k, v, attn_mask=mask)
+    assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=mask), kern)
+    assert torch.equal(sageattention.sageattn(q, k, v, attn_mask=mask), kern)
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=mask)
+    assert cosine(kern.float().cpu().numpy(), ref.cpu().numpy()) >= COS
+    fmask = torch.zeros(1, 1, 1, 1024, device=dev, dtype=torch.bfloat16)
+    fmask[..., 900:] = float("-inf")
+    sd = cdna4_sage._torch_sdpa(q, k, v, attn_mask=fmask)
+    assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=fmask), sd)
+    monkeypatch.setattr(cdna4_sage, "NATIVE_MASK", False)
+    assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=mask), cdna4_sage._torch_sdpa(q, k, v, attn_mask=mask))
+
+
+def test_masked_op_and_graph_capture(dev):
+    """torch.ops.cdna4_sage.attention_masked is the same call, and the masked forward (mask preparation, quantizers,
+    attention, merge) replays under a HIP graph with the eager result on every replay."""
+    q, k, v = (t.to(dev) for t in _inputs(1, 4, 4, 520, 520, 128, torch.bfloat16, "HND", seed=8))
+    mask = _random((1, 1, 520, 520), 0.75, 9).to(dev)
+    eager = cdna4_sage.attention(q, k, v, attn_mask=mask)
+    op = torch.ops.cdna4_sage.attention_masked(q, k, v, mask, "HND", 0.0, False)
+    assert torch.equal(op.transpose(1, 2), eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        cdna4_sage.attention(q, k, v, attn_mask=mask)           # warm-up: workspace sizes cached, allocator primed
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gout = cdna4_sage.attention(q, k, v, attn_mask=mask)
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, eager), i
+        cdna4_sage.attention(q, k, v)                              # eager work between replays
+        torch.cuda.synchronize()

@@ -383,6 +383,64 @@ def test_split_emulation_gives_exact_lse_and_matches_unsplit():
         assert np.abs(out - 1.0).max() < 1e-2, chunks
 
 
+def test_mask_identities():
+    """Boolean attn_mask pins: an all-True mask is no mask; the bottom-right triangle as a mask is the causal flag; a
+    key-padding mask equals the call on the shorter key range with the same quantized K / V (per-row softmax state
+    never sees a masked key); a row whose mask is all False is 0 (and no NaN reaches the other rows)."""
+    q, k, v = _bf16((2, 3, 90, 64), 60), _bf16((2, 3, 150, 64), 61), _bf16((2, 3, 150, 64), 62)
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    base = orc.attention(q8, qs, k8, ks, v8, vs, 150, block_n=64, out_dtype="f32")
+    allt = orc.attention(q8, qs, k8, ks, v8, vs, 150, block_n=64, out_dtype="f32", attn_mask=np.ones((150,), bool))
+    assert np.array_equal(base, allt)
+    causal = orc.attention(q8, qs, k8, ks, v8, vs, 150, causal=True, block_n=64, out_dtype="f32")
+    tri = np.arange(150)[None, :] <= np.arange(90)[:, None] + 60
+    assert np.array_equal(causal, orc.attention(q8, qs, k8, ks, v8, vs, 150, block_n=64, out_dtype="f32",
+                                                attn_mask=tri))
+    # causal flag and a mask together: the AND of both
+    half = np.arange(150) % 2 == 0
+    assert np.array_equal(orc.attention(q8, qs, k8, ks, v8, vs, 150, causal=True, block_n=64, out_dtype="f32",
+                                        attn_mask=half),
+                          orc.attention(q8, qs, k8, ks, v8, vs, 150, block_n=64, out_dtype="f32",
+                                        attn_mask=tri & half))
+    for n in (1, 64, 100):          # one key, a whole tile, a partial tile
+        pad = np.arange(150)[None, None, None, :] < n
+        short = orc.attention(q8, qs, k8, ks, v8, vs, n, block_n=64, out_dtype="f32")
+        assert np.array_equal(short, orc.attention(q8, qs, k8, ks, v8, vs, 150, block_n=64, out_dtype="f32",
+                                                   attn_mask=pad)), n
+    rowmask = np.ones((2, 1, 90, 150), bool)
+    rowmask[1, :, 7] = False
+    out = orc.attention(q8, qs, k8, ks, v8, vs, 150, block_n=64, out_dtype="f32", attn_mask=rowmask)
+    assert np.isfinite(out).all() and (out[1, :, 7] == 0).all()
+    assert np.array_equal(np.delete(out, 7, axis=2), np.delete(base, 7, axis=2))
+
+
+def test_masked_emulation_vs_float64_and_split():
+    """A random mask (a third of the keys hidden, per batch, head and row), with and without the causal flag: the
+    quantized path stays within the accuracy of the unmasked one against the float64 masked softmax, and split key
+    ranges (including ranges in which a row sees no key, and rows that see no key at all) merge to the unsplit
+    result up to the fp16 rounding of the stored O / l."""
+    rng = np.random.default_rng(63)
+    q, k, v = _bf16((1, 2, 70, 128), 64), _bf16((1, 2, 260, 128), 65), _bf16((1, 2, 260, 128), 66)
+    mask = rng.random((1, 2, 70, 260)) > 0.33
+    mask[0, 0, 5, :] = False                         # a row that sees nothing
+    mask[0, 1, 9, :] = False
+    mask[0, 1, 9, 250] = True                        # a row that sees one key of the last tile only
+    for causal in (False, True):
+        out = orc.sage_forward(q, k, v, causal=causal, block_n=64, out_dtype="f32", attn_mask=mask)
+        ref = orc.sdpa_reference(q, k, v, causal=causal, attn_mask=mask)
+        assert np.isfinite(out).all() and (out[0, 0, 5] == 0).all() and (ref[0, 0, 5] == 0).all()
+        assert _cos(out, ref) >= 0.999, causal
+        rows = np.ones((1, 2, 70), dtype=bool)
+        for chunks in (2, 5):
+            sp = orc.sage_forward(q, k, v, causal=causal, block_n=64, out_dtype="f32", attn_mask=mask,
+                                  kv_split=(chunks, rows))
+            assert np.isfinite(sp).all() and (sp[0, 0, 5] == 0).all()
+            assert _cos(sp, ref) >= _cos(out, ref) - 1e-4, (causal, chunks)
+            # row 9 of head 1 sees one key, in the last range: the merge must return that range alone
+            assert np.abs(sp[0, 1, 9] - out[0, 1, 9]).max() <= 2.0 ** -10 * np.abs(out[0, 1, 9]).max() + 1e-6
+
+
 def test_split_rows_numbering():
     r = orc.split_rows(2, 3, 300, n_full=7)          # q_tiles = 3: tile = (b * 3 + h) * 3 + row // 128
     assert r.shape == (2, 3, 300)

@@ -11,6 +11,8 @@ from pathlib import Path
 
 import pytest
 
+from cdna4_sage import _capi
+
 ROOT = Path(__file__).resolve().parent.parent
 LIB = ROOT / "rdna4-sageattention_amd" / "cdna4_sage" / "libsage_capi.so"
 
@@ -53,5 +55,5 @@ def test_unpacked_wheel_imports_its_own_library(wheel, tmp_path):
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=tmp_path,
                          timeout=300, check=True).stdout.strip()
     abi, *rest = out.split(" ", 1)
-    assert int(abi) == 3 and "(64, 96, 128, 256)" in rest[0]
+    assert int(abi) == _capi.ABI_VERSION and "(64, 96, 128, 256)" in rest[0]
     assert str(tmp_path) in rest[0]
