@@ -52,6 +52,12 @@ __device__ __forceinline__ void copy16_to_lds(const void* g, void* lds) {
                                    (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
+// 32-bit load through the global address space (a generic pointer would give a flat load, which also counts on the
+// LDS counter, so every LDS wait of the tile would wait for it)
+__device__ __forceinline__ uint32_t load_global_u32(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) uint32_t*)(p);
+}
+
 constexpr int ATT_MAX_CHUNKS = 16;
 
 // Workspace of a split launch (units = split tiles x chunks): each chunk's O normalised by its own l, as fp16
@@ -80,7 +86,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
     int Sq_arg, int Skv_arg, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part,
-    float c0, int dout, VarlenTiles vt, MaskTabs mt) {
+    float c0, int dout, VarlenTiles vt, MaskTabs mt, const uint32_t* __restrict__ mbits_tab,
+    const int* __restrict__ mcls_tab, const int2* __restrict__ mrange_tab) {
   static_assert(!(MASK && (CAUSAL || VARLEN)), "the mask variant folds causality into its bits and is dense only");
   constexpr int BN = ATT_BN;
   constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
@@ -163,35 +170,19 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     t_hi = (ch + 1) * ntiles / chunks;
   }
 
-  // ---- mask: this lane's bit row and this wave's class row; the workgroup skips the tiles before the first and
-  // after the last tile that any of its rows sees (the skipped tiles hold no visible key, so skipping them is
+  // ---- mask: this lane's bit row and this wave's class row; the workgroup runs only the tiles from the first to the
+  // last that any of its rows sees (mask_range_kernel; the tiles outside hold no visible key, so skipping them is
   // exactly the online softmax over them) ----
   const uint8_t* mbase = nullptr;  // this (batch, head)'s mask words; the lane's row at byte offset moff
-  uint32_t moff = 0;                 // (the bits array is below 2 GiB, checked on the host)
+  uint32_t moff = 0;                 // (a (batch, head) slice of the bits is below 2 GiB, checked on the host)
   const int* mcls = nullptr;
   if (MASK) {
-    mbase = reinterpret_cast<const uint8_t*>(mt.bits + (int64_t)b * mt.bsb + (int64_t)h * mt.bsh);
+    mbase = reinterpret_cast<const uint8_t*>(mbits_tab + (int64_t)b * mt.bsb + (int64_t)h * mt.bsh);
     moff = (uint32_t)(((int64_t)qr * mt.bsq + hf) * 4);
-    mcls = mt.cls + (int64_t)b * mt.csb + (int64_t)h * mt.csh + (int64_t)min(q0 >> 5, mt.groups - 1) * mt.csg;
-    __shared__ int mrange[2];
-    if (threadIdx.x == 0) {
-      mrange[0] = ntiles;
-      mrange[1] = -1;
-    }
-    __syncthreads();
-    int lo = ntiles, hi = -1;
-    for (int t = lane; t < ntiles; t += 64)
-      if (mcls[t] != 0) {
-        lo = min(lo, t);
-        hi = max(hi, t);
-      }
-    if (hi >= 0) {
-      atomicMin(&mrange[0], lo);
-      atomicMax(&mrange[1], hi);
-    }
-    __syncthreads();
-    t_lo = max(t_lo, mrange[0]);
-    t_hi = min(t_hi, mrange[1] + 1);
+    mcls = mcls_tab + (int64_t)b * mt.csb + (int64_t)h * mt.csh + (int64_t)min(q0 >> 5, mt.groups - 1) * mt.csg;
+    const int2 r = mrange_tab[(int64_t)b * mt.rsb + (int64_t)h * mt.rsh + min(qt, mt.rblocks - 1)];
+    t_lo = max(t_lo, r.x);
+    t_hi = min(t_hi, r.y);
   }
 
   const int8_t* kbase = k8 + ((int64_t)khead * Skp + kofs) * D;
@@ -350,9 +341,9 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     // per wave and tile: skip (class 0), the mask-free body (1) or the bit-masked body (2).  Runs of tiles of
     // classes 0 / 1 and runs of class 2 go through two loops with one tile body each (one loop holding both bodies
     // spills); each iteration of either ends in the workgroup barrier of its tile, and s_barrier counts waves, not
-    // program locations, so the waves of a workgroup may sit in different loops.  The class of the next tile is
-    // loaded one iteration ahead (scalar); the lane's mask word is loaded before the next tile's direct loads are
-    // issued, so the wait for it (after the QK MFMAs) does not wait for the tile data.
+    // program locations, so the waves of a workgroup may sit in different loops.  The class of the next tile
+    // (scalar) and, inside a run of class 2, the lane's mask word of the next tile are loaded one iteration ahead, so
+    // the end-of-tile wait for the direct loads covers them and no wait inside a tile waits for the next tile.
     int c_nxt = t < t_hi ? mcls[t] : 0;
     while (t < t_hi) {
       for (; t < t_hi && c_nxt != 2; ++t) {
@@ -365,17 +356,26 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
-      for (; t < t_hi && c_nxt == 2; ++t) {
+      if (t < t_hi) {  // a run of class 2 (its first word is waited for once)
         const uint8_t* mb_ = mbase;
         asm volatile("" : "+s"(mb_));
-        const uint32_t mw_ = *reinterpret_cast<const uint32_t*>(mb_ + (moff + 8u * (uint32_t)t));
-        if (t + 1 < t_hi) {
-          c_nxt = mcls[t + 1];
-          SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+        uint32_t mw_cur = load_global_u32(mb_ + (moff + 8u * (uint32_t)t));
+        // the uses below make the compiler's own waits for the words fall where the words are known to be complete
+        // (here, and after the end-of-tile wait), not inside the next tile
+        asm volatile("" ::"v"(mw_cur));
+        for (; t < t_hi && c_nxt == 2; ++t) {
+          uint32_t mw_nxt = 0u;
+          if (t + 1 < t_hi) {
+            mw_nxt = load_global_u32(mb_ + (moff + 8u * (uint32_t)(t + 1)));
+            c_nxt = mcls[t + 1];
+            SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+          }
+          SAGE_TILE(t, 2, mw_cur);
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          asm volatile("" ::"v"(mw_nxt));
+          __syncthreads();
+          mw_cur = mw_nxt;
         }
-        SAGE_TILE(t, 2, mw_);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
       }
     }
   } else {
@@ -602,7 +602,7 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
                      vs, o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks,
-                     part, c0, hd, VarlenTiles{}, MaskTabs{});
+                     part, c0, hd, VarlenTiles{}, MaskTabs{}, nullptr, nullptr, nullptr);
   if (n_split > 0) {
     if ((rc = check_launch("attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
@@ -670,7 +670,8 @@ static int launch_attn_varlen(const int8_t* q8, const float* qs, const int8_t* k
                               int TQ, int TKP, int hd, int n_blocks, VarlenTiles vt, hipStream_t st) {
   hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
                      v8t, vs, static_cast<uint16_t*>(out), (int64_t)0, oss, osh, nullptr, H, Hkv, TQ, 0, TKP, 0,
-                     n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt, MaskTabs{});
+                     n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt, MaskTabs{}, nullptr, nullptr,
+                     nullptr);
   return check_launch("varlen attention launch");
 }
 
@@ -715,7 +716,7 @@ static int launch_attn_mask(const int8_t* q8, const float* qs, const int8_t* k8,
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL((attn_kernel<D, false, OUT_DT, false, true>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8,
                      ks, v8t, vs, o, osb, oss, osh, nullptr, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles,
-                     p.n_full, p.chunks, part, c0, hd, VarlenTiles{}, mt);
+                     p.n_full, p.chunks, part, c0, hd, VarlenTiles{}, mt, mt.bits, mt.cls, mt.range);
   if (n_split > 0) {
     if ((rc = check_launch("masked attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,

@@ -7,7 +7,9 @@
 //         accumulator (bit 16 kb + v <-> key 64 t + 32 kb + 8 (v / 4) + 4 hf + v % 4), so the kernel masks a score
 //         with one bit extract and one bit select;
 //   cls   one entry per (32-row group, tile): 0 = no row sees a key of the tile (the wave skips it), 1 = every row
-//         sees every key (the mask-free tile body), 2 = mixed (the bit-masked body).
+//         sees every key (the mask-free tile body), 2 = mixed (the bit-masked body);
+//   range one (first, last + 1) tile pair per 128-row block (an attention workgroup's rows): the tiles outside it
+//         are not visited at all.
 // Keys past kv_len and, with the causal flag, keys past the bottom-right diagonal are folded into the bits.
 #include "sage_common.h"
 #include "sage_host.h"
@@ -26,8 +28,8 @@ int attn_mask_impl(const int8_t* q8, const float* qs, const int8_t* k8, const fl
 // Extents of the tables.  A mask axis with stride 0 (broadcast) is stored once; rows are stored when the mask has a
 // row axis or the causal flag makes rows differ.
 struct MaskShape {
-  int mb, mh, mq, mg, nt;
-  int64_t bits_words, cls_entries;
+  int mb, mh, mq, mg, nt, nrb;
+  int64_t bits_words, cls_entries, range_entries;
 };
 
 static MaskShape mask_shape(int B, int H, int Sq, int Skv, int64_t msb, int64_t msh, int64_t msq, int causal) {
@@ -37,18 +39,20 @@ static MaskShape mask_shape(int B, int H, int Sq, int Skv, int64_t msb, int64_t 
   const bool rows = msq != 0 || causal;
   m.mq = rows ? Sq : 1;
   m.mg = rows ? (Sq + 31) / 32 : 1;
+  m.nrb = rows ? (Sq + 127) / 128 : 1;
   m.nt = (Skv + 63) / 64;
   m.bits_words = (int64_t)m.mb * m.mh * m.mq * m.nt * 2;
   m.cls_entries = (int64_t)m.mb * m.mh * m.mg * m.nt;
+  m.range_entries = (int64_t)m.mb * m.mh * m.nrb;
   return m;
 }
 
 static int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
-// Workspace of sage_forward_masked: the attention plan's split state, the per-chunk V maxima, the bits, the classes
-// (each 256-byte aligned).
+// Workspace of sage_forward_masked: the attention plan's split state, the per-chunk V maxima, the bits, the classes,
+// the ranges (each 256-byte aligned).
 struct MaskWorkspace {
-  int64_t attn, vpart, bits, cls, total;
+  int64_t attn, vpart, bits, cls, range, total;
 };
 
 static int mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, const MaskShape& m, MaskWorkspace* w) {
@@ -57,7 +61,8 @@ static int mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, const M
   w->vpart = align256(w->attn);
   w->bits = w->vpart + align256(vamax_partial_bytes(B, Hkv, Skv, D));
   w->cls = w->bits + align256(m.bits_words * 4);
-  w->total = w->cls + align256(m.cls_entries * 4);
+  w->range = w->cls + align256(m.cls_entries * 4);
+  w->total = w->range + align256(m.range_entries * 8);
   return SAGE_OK;
 }
 
@@ -114,8 +119,34 @@ __global__ __launch_bounds__(256) void mask_prep_kernel(const uint8_t* __restric
   if (lane == 0) cls[((int64_t)mbh * mg + g) * nt + t] = any == 0 ? 0 : (all == ~0ull ? 1 : 2);
 }
 
+// One wave per (mask batch-head, 128-row block): the first and one past the last tile whose class is not 0 in any of
+// the block's four 32-row groups (groups past the last one repeat it), (nt, 0) when there is none.  Lanes scan the
+// 4 x nt classes with all their loads in flight, then a wave reduction.  grid = ceil(n / 4) blocks of 256 threads,
+// n = mb * mh * nrb.
+__global__ __launch_bounds__(256) void mask_range_kernel(const int* __restrict__ cls, int mg, int nt, int nrb, int n,
+                                                         int2* __restrict__ range) {
+  const int wid = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (wid >= n) return;  // the whole wave
+  const int lane = threadIdx.x & 63;
+  const int mbh = wid / nrb, rb = wid % nrb;
+  int lo = nt, hi = -1;
+  for (int i = lane; i < 4 * nt; i += 64) {
+    const int g = min(rb * 4 + i / nt, mg - 1), t = i % nt;
+    if (cls[((int64_t)mbh * mg + g) * nt + t] != 0) {
+      lo = min(lo, t);
+      hi = max(hi, t);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo = min(lo, __shfl_xor(lo, o));
+    hi = max(hi, __shfl_xor(hi, o));
+  }
+  if (lane == 0) range[wid] = make_int2(lo, hi + 1);
+}
+
 static int launch_mask_prep(const void* mask, int64_t msb, int64_t msh, int64_t msq, int Sq, int Skv, int causal,
-                            const MaskShape& m, uint32_t* bits, int* cls, hipStream_t st) {
+                            const MaskShape& m, uint32_t* bits, int* cls, int2* range, hipStream_t st) {
   const bool a4 = ((uintptr_t)mask & 3u) == 0 && msb % 4 == 0 && msh % 4 == 0 && msq % 4 == 0;
   const int64_t blocks = (int64_t)m.mb * m.mh * m.mg * ((m.nt + 3) / 4);
   const uint8_t* mp = static_cast<const uint8_t*>(mask);
@@ -125,6 +156,9 @@ static int launch_mask_prep(const void* mask, int64_t msb, int64_t msh, int64_t 
   else
     hipLaunchKernelGGL(mask_prep_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, mp, msb, msh, msq, m.mh,
                        m.mq, m.mg, m.nt, Sq, Skv, causal, bits, cls);
+  const int n = (int)m.range_entries;
+  hipLaunchKernelGGL(mask_range_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, cls, m.mg, m.nt, m.nrb, n,
+                     range);
   return check_launch("mask preparation launch");
 }
 
@@ -191,20 +225,26 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
   char* ws = static_cast<char*>(workspace);
   uint32_t* bits = reinterpret_cast<uint32_t*>(ws + w.bits);
   int* cls = reinterpret_cast<int*>(ws + w.cls);
+  int2* range = reinterpret_cast<int2*>(ws + w.range);
   float* vpart = reinterpret_cast<float*>(ws + w.vpart);
   if ((rc = sage::forward_quant_impl(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype,
                                      qs_mul, q8, qs, vpart, k8, ks, v8t, vs, stream)))
     return rc;
-  if ((rc = sage::launch_mask_prep(mask, msb, msh, msq, Sq, Skv, causal, m, bits, cls, (hipStream_t)stream))) return rc;
+  if ((rc = sage::launch_mask_prep(mask, msb, msh, msq, Sq, Skv, causal, m, bits, cls, range, (hipStream_t)stream)))
+    return rc;
   const sage::MaskTabs mt{bits,
                           cls,
+                          range,
                           m.mb > 1 ? (int64_t)m.mh * m.mq * m.nt * 2 : 0,
                           m.mh > 1 ? (int64_t)m.mq * m.nt * 2 : 0,
                           m.mq > 1 ? (int64_t)m.nt * 2 : 0,
                           m.mb > 1 ? (int64_t)m.mh * m.mg * m.nt : 0,
                           m.mh > 1 ? (int64_t)m.mg * m.nt : 0,
                           m.mg > 1 ? (int64_t)m.nt : 0,
-                          m.mg};
+                          m.mb > 1 ? (int64_t)m.mh * m.nrb : 0,
+                          m.mh > 1 ? (int64_t)m.nrb : 0,
+                          m.mg,
+                          m.nrb};
   return sage::attn_mask_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, dtype, &mt,
                               w.attn ? workspace : nullptr, stream);
 }
