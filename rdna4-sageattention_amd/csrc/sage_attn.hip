@@ -275,13 +275,15 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
           sf_[kb_][v_] = __int_as_float((__float_as_int(sf_[kb_][v_]) & keep_) | (int)(0xFF800000u & ~(uint32_t)keep_)); \
         }                                                                                                  \
     }                                                                                                      \
-    float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                              \
+    /* block maxima on the bit patterns: the scores are positive floats (1.5 * 2^23 + S) or -inf, whose int32   \
+       patterns order like the floats, and an integer max needs no NaN canonicalisation */                  \
+    int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                               \
     _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                    \
-      mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                      \
-      mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                      \
+      mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                        \
+      mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                        \
     }                                                                                                      \
-    mx0_ = fmaxf(mx0_, xor32_f32(mx0_));                                                                   \
-    mx1_ = fmaxf(mx1_, xor32_f32(mx1_));                                                                   \
+    const float mx0_ = __int_as_float(max(mi0_, xor32_i32(mi0_)));                                         \
+    const float mx1_ = __int_as_float(max(mi1_, xor32_i32(mi1_)));                                         \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
     const float rowmax_ = fmaxf((mx0_ - SEED_F) * ks0_, (mx1_ - SEED_F) * ks1_);                           \
     const float mcand_ = fmaxf(m, rowmax_);                                                                \

@@ -31,9 +31,10 @@ int attn_impl(const int8_t*, const float*, const int8_t*, const float*, const ui
               int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*, int64_t, void*);
 int attn_plan_impl(int, int, int, int, int, int, int*, int*, int64_t*);
 int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D);
+struct MaskPrep;
 int forward_quant_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, const void*,
                        int64_t, int64_t, int64_t, int, int, int, int, int, int, int, float, int8_t*, float*, float*,
-                       int8_t*, float*, uint8_t*, float*, void*);
+                       int8_t*, float*, uint8_t*, float*, const MaskPrep*, void*);
 
 // sage_forward's workspace: the attention plan's partial state, then (256-byte aligned) the per-chunk V maxima.
 static int forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t* attn_bytes,
@@ -109,7 +110,7 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
   SAGE_REQUIRE(((uintptr_t)workspace & 255u) == 0, "sage_forward: workspace must be 256-byte aligned");
   float* vpart = reinterpret_cast<float*>(static_cast<char*>(workspace) + (attn_bytes + 255) / 256 * 256);
   if ((rc = sage::forward_quant_impl(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype,
-                                     qs_mul, q8, qs, vpart, k8, ks, v8t, vs, stream)))
+                                     qs_mul, q8, qs, vpart, k8, ks, v8t, vs, nullptr, stream)))
     return rc;
   return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype, nullptr,
                          attn_bytes ? workspace : nullptr, attn_bytes, stream);

@@ -64,10 +64,11 @@ template <int CTRL> __device__ __forceinline__ double dpp_f64(double x) {
   return __hiloint2double(phi, plo);
 }
 // value held by lane (lane ^ 32)
-__device__ __forceinline__ float xor32_f32(float x) {
+__device__ __forceinline__ int xor32_i32(int x) {
   const int lane = __lane_id();
-  return __int_as_float(__builtin_amdgcn_ds_bpermute(((lane ^ 32) << 2), __float_as_int(x)));
+  return __builtin_amdgcn_ds_bpermute(((lane ^ 32) << 2), x);
 }
+__device__ __forceinline__ float xor32_f32(float x) { return __int_as_float(xor32_i32(__float_as_int(x))); }
 
 // ---- Hadamard (float64 FWHT) -----------------------------------------------------------------------------------
 // x holds EPL consecutive elements of a row whose other slices sit in the 1 / 2 / 4 neighbouring lanes of a quad

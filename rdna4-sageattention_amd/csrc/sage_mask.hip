@@ -1,5 +1,5 @@
-// Boolean attention masks (torch SDPA's bool attn_mask, True = attend): the bit and class tables that the mask
-// variant of attn_kernel reads, and the one-call masked forward.
+// Boolean attention masks (torch SDPA's bool attn_mask, True = attend): the tables that the mask variant of
+// attn_kernel reads, and the one-call masked forward.
 //
 // The reference has no masked kernel: src/rdna4_sage/__init__.py:78-79 sends every call with an attn_mask to torch
 // SDPA.  Here the mask is turned, on the GPU and in the call's stream, into
@@ -10,15 +10,16 @@
 //         sees every key (the mask-free tile body), 2 = mixed (the bit-masked body);
 //   range one (first, last + 1) tile pair per 128-row block (an attention workgroup's rows): the tiles outside it
 //         are not visited at all.
-// Keys past kv_len and, with the causal flag, keys past the bottom-right diagonal are folded into the bits.
-#include "sage_common.h"
-#include "sage_host.h"
+// Keys past kv_len and, with the causal flag, keys past the bottom-right diagonal are folded into the bits.  The
+// tables are built by extra workgroups of the two quantization launches (sage_mask.h), so a masked call has the
+// launches of an unmasked one.
+#include "sage_mask.h"
 
 namespace sage {
 
 int forward_quant_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, const void*,
                        int64_t, int64_t, int64_t, int, int, int, int, int, int, int, float, int8_t*, float*, float*,
-                       int8_t*, float*, uint8_t*, float*, void*);
+                       int8_t*, float*, uint8_t*, float*, const MaskPrep*, void*);
 int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D);
 int attn_mask_plan_impl(int B, int H, int Sq, int Skv, int D, int64_t* ws);
 int attn_mask_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
@@ -64,102 +65,6 @@ static int mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, const M
   w->range = w->cls + align256(m.cls_entries * 4);
   w->total = w->range + align256(m.range_entries * 8);
   return SAGE_OK;
-}
-
-// One wave per (mask batch-head, 32-row group, tile): lane (row r = lane % 32 of the group, half hf = lane / 32)
-// builds its word from the 32 mask bytes of its keys (8 runs of 4 consecutive keys: run j holds keys
-// 64 t + 8 j + 4 hf + i at bits 4 j + i); two ballots over the wave give the class.  Rows past q_len (and, for a
-// mask without rows, every row but 0) count as neither seeing nor missing a key.  A4: mask rows start 4-byte
-// aligned, so a run inside kv_len is one 32-bit load.  grid = mb * mh * mg * ceil(nt / 4) blocks of 256 threads.
-template <bool A4>
-__global__ __launch_bounds__(256) void mask_prep_kernel(const uint8_t* __restrict__ mask, int64_t msb, int64_t msh,
-                                                        int64_t msq, int mh, int mq, int mg, int nt, int Sq, int Skv,
-                                                        int causal, uint32_t* __restrict__ bits,
-                                                        int* __restrict__ cls) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = lane & 31, hf = lane >> 5;
-  const int ntb = (nt + 3) >> 2;
-  const int t = (int)(blockIdx.x % ntb) * 4 + wave;
-  const int rest = (int)(blockIdx.x / ntb);
-  const int g = rest % mg;
-  const int mbh = rest / mg;
-  if (t >= nt) return;  // the whole wave
-  const int mbi = mbh / mh, mhi = mbh % mh;
-  const int q = g * 32 + r;  // table row (mq == 1: row 0 only)
-  const bool real = mq == 1 ? r == 0 : q < Sq;
-  uint32_t w = 0;
-  if (real) {
-    const uint8_t* row = mask + mbi * msb + mhi * msh + (int64_t)q * msq;
-    const int lim = causal ? min(Skv - 1, q + (Skv - Sq)) : Skv - 1;  // last key the row may see
-    const int k0 = t * 64 + 4 * hf;
-    uint32_t b4[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kj = k0 + 8 * j;
-      if (A4 && kj + 3 < Skv) {
-        b4[j] = *reinterpret_cast<const uint32_t*>(row + kj);
-      } else {
-        b4[j] = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (kj + i < Skv) b4[j] |= (uint32_t)row[kj + i] << (8 * i);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool vis = ((b4[j] >> (8 * i)) & 0xFFu) != 0 && k0 + 8 * j + i <= lim;
-        w |= (uint32_t)vis << (4 * j + i);
-      }
-    bits[(((int64_t)mbh * mq + q) * nt + t) * 2 + hf] = w;
-  }
-  const uint64_t any = __ballot(real && w != 0);
-  const uint64_t all = __ballot(!real || w == 0xFFFFFFFFu);
-  if (lane == 0) cls[((int64_t)mbh * mg + g) * nt + t] = any == 0 ? 0 : (all == ~0ull ? 1 : 2);
-}
-
-// One wave per (mask batch-head, 128-row block): the first and one past the last tile whose class is not 0 in any of
-// the block's four 32-row groups (groups past the last one repeat it), (nt, 0) when there is none.  Lanes scan the
-// 4 x nt classes with all their loads in flight, then a wave reduction.  grid = ceil(n / 4) blocks of 256 threads,
-// n = mb * mh * nrb.
-__global__ __launch_bounds__(256) void mask_range_kernel(const int* __restrict__ cls, int mg, int nt, int nrb, int n,
-                                                         int2* __restrict__ range) {
-  const int wid = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-  if (wid >= n) return;  // the whole wave
-  const int lane = threadIdx.x & 63;
-  const int mbh = wid / nrb, rb = wid % nrb;
-  int lo = nt, hi = -1;
-  for (int i = lane; i < 4 * nt; i += 64) {
-    const int g = min(rb * 4 + i / nt, mg - 1), t = i % nt;
-    if (cls[((int64_t)mbh * mg + g) * nt + t] != 0) {
-      lo = min(lo, t);
-      hi = max(hi, t);
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    lo = min(lo, __shfl_xor(lo, o));
-    hi = max(hi, __shfl_xor(hi, o));
-  }
-  if (lane == 0) range[wid] = make_int2(lo, hi + 1);
-}
-
-static int launch_mask_prep(const void* mask, int64_t msb, int64_t msh, int64_t msq, int Sq, int Skv, int causal,
-                            const MaskShape& m, uint32_t* bits, int* cls, int2* range, hipStream_t st) {
-  const bool a4 = ((uintptr_t)mask & 3u) == 0 && msb % 4 == 0 && msh % 4 == 0 && msq % 4 == 0;
-  const int64_t blocks = (int64_t)m.mb * m.mh * m.mg * ((m.nt + 3) / 4);
-  const uint8_t* mp = static_cast<const uint8_t*>(mask);
-  if (a4)
-    hipLaunchKernelGGL(mask_prep_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, mp, msb, msh, msq, m.mh, m.mq,
-                       m.mg, m.nt, Sq, Skv, causal, bits, cls);
-  else
-    hipLaunchKernelGGL(mask_prep_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, mp, msb, msh, msq, m.mh,
-                       m.mq, m.mg, m.nt, Sq, Skv, causal, bits, cls);
-  const int n = (int)m.range_entries;
-  hipLaunchKernelGGL(mask_range_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, cls, m.mg, m.nt, m.nrb, n,
-                     range);
-  return check_launch("mask preparation launch");
 }
 
 static int check_mask_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t msb, int64_t msh,
@@ -227,10 +132,28 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
   int* cls = reinterpret_cast<int*>(ws + w.cls);
   int2* range = reinterpret_cast<int2*>(ws + w.range);
   float* vpart = reinterpret_cast<float*>(ws + w.vpart);
+  sage::MaskPrep mp;
+  mp.mask = static_cast<const uint8_t*>(mask);
+  mp.msb = msb;
+  mp.msh = msh;
+  mp.msq = msq;
+  mp.mh = m.mh;
+  mp.mq = m.mq;
+  mp.mg = m.mg;
+  mp.nt = m.nt;
+  mp.nrb = m.nrb;
+  mp.Sq = Sq;
+  mp.Skv = Skv;
+  mp.causal = causal;
+  mp.a4 = ((uintptr_t)mask & 3u) == 0 && msb % 4 == 0 && msh % 4 == 0 && msq % 4 == 0;
+  mp.bits = bits;
+  mp.cls = cls;
+  mp.range = range;
+  mp.nrange = (int)m.range_entries;
+  mp.prep_blocks = (int)((int64_t)m.mb * m.mh * m.mg * ((m.nt + 3) / 4));
+  mp.range_blocks = (mp.nrange + 3) / 4;
   if ((rc = sage::forward_quant_impl(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype,
-                                     qs_mul, q8, qs, vpart, k8, ks, v8t, vs, stream)))
-    return rc;
-  if ((rc = sage::launch_mask_prep(mask, msb, msh, msq, Sq, Skv, causal, m, bits, cls, range, (hipStream_t)stream)))
+                                     qs_mul, q8, qs, vpart, k8, ks, v8t, vs, &mp, stream)))
     return rc;
   const sage::MaskTabs mt{bits,
                           cls,

@@ -15,6 +15,7 @@
 // 128-channel layout.
 #include "sage_common.h"
 #include "sage_host.h"
+#include "sage_mask.h"
 
 namespace sage {
 
@@ -290,29 +291,40 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
 #pragma unroll
     for (int i = 0; i < 8; ++i) am[i] = am_src[c8 * 8 + i];
   } else {
+    // the per-chunk maxima are reduced once per block: thread (4-channel group cg, slice cs) takes the maximum of
+    // chunks cs, cs + NSL, ... (all its loads in flight), the slices meet in LDS, and one row of threads reduces
+    // them (and stores VS when vs_out is set); every thread then reads its 8 channels.
+    constexpr int NCG = DP / 4, NSL = 256 / NCG, PER = (V_AMAX_CHUNKS + NSL - 1) / NSL;
+    __shared__ __attribute__((aligned(16))) float vpart_lds[NSL][DP];
+    const int cg = threadIdx.x % NCG, cs = threadIdx.x / NCG;
+    v4f pc[PER];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) am[i] = 0.0f;
-    // all (at most V_AMAX_CHUNKS) rows of maxima in flight at once; indices past the last chunk repeat it, which a
-    // max does not notice
-    v4f pa[V_AMAX_CHUNKS], pb[V_AMAX_CHUNKS];
+    for (int i = 0; i < PER; ++i)  // chunks past the last one repeat it, which a maximum does not notice
+      pc[i] = *reinterpret_cast<const v4f*>(am_src + (int64_t)min(cs + i * NSL, vchunks - 1) * DP + 4 * cg);
+    v4f m4 = pc[0];
 #pragma unroll
-    for (int c = 0; c < V_AMAX_CHUNKS; ++c) {
-      const v4f* p4 = reinterpret_cast<const v4f*>(am_src + (int64_t)min(c, vchunks - 1) * DP + c8 * 8);
-      pa[c] = p4[0];
-      pb[c] = p4[1];
-    }
+    for (int i = 1; i < PER; ++i)
 #pragma unroll
-    for (int c = 0; c < V_AMAX_CHUNKS; ++c) {
+      for (int e = 0; e < 4; ++e) m4[e] = fmaxf(m4[e], pc[i][e]);
+    *reinterpret_cast<v4f*>(&vpart_lds[cs][4 * cg]) = m4;
+    __syncthreads();
+    if (cs == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        am[i] = fmaxf(am[i], pa[c][i]);
-        am[4 + i] = fmaxf(am[4 + i], pb[c][i]);
+      for (int j = 1; j < NSL; ++j) {
+        const v4f o4 = *reinterpret_cast<const v4f*>(&vpart_lds[j][4 * cg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m4[e] = fmaxf(m4[e], o4[e]);
       }
+      *reinterpret_cast<v4f*>(&vpart_lds[0][4 * cg]) = m4;
+      if (vs_out != nullptr) *reinterpret_cast<v4f*>(vs_out + 4 * cg) = m4;
     }
-    if (vs_out != nullptr && r0 == 0) {
-      v4f* o4 = reinterpret_cast<v4f*>(vs_out + c8 * 8);
-      o4[0] = v4f{am[0], am[1], am[2], am[3]};
-      o4[1] = v4f{am[4], am[5], am[6], am[7]};
+    __syncthreads();
+    const v4f a0 = *reinterpret_cast<const v4f*>(&vpart_lds[0][c8 * 8]);
+    const v4f a1 = *reinterpret_cast<const v4f*>(&vpart_lds[0][c8 * 8 + 4]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      am[i] = a0[i];
+      am[4 + i] = a1[i];
     }
   }
   float cs[8];
@@ -385,8 +397,8 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
 }
 
 // sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (vamax_chunk_rows keys each) to `vpart`,
-// blocks [nv, nv + nk) quantize 64 keys of K each, the rest quantize Q.  The V blocks come first so their longer row
-// loops start early.
+// blocks [nv, nv + nk) quantize 64 keys of K each, the next nq quantize Q, and sage_forward_masked's mask blocks
+// (mp.prep_blocks of them) follow.  The V blocks come first so their longer row loops start early.
 template <int D, int DT>
 __global__ __launch_bounds__(256) void quant_qk_vamax_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
                                                              int64_t sh, int H, int Sq, int row_tiles, float qs_mul,
@@ -395,14 +407,17 @@ __global__ __launch_bounds__(256) void quant_qk_vamax_kernel(const uint16_t* __r
                                                              int64_t ksh, int Skp, int nk, int8_t* __restrict__ k8,
                                                              float* __restrict__ ks, const uint16_t* __restrict__ v,
                                                              int64_t vsb, int64_t vss, int64_t vsh, int Hkv, int Skv,
-                                                             int vchunks, int nv, float* __restrict__ vpart) {
+                                                             int vchunks, int nv, float* __restrict__ vpart, int nq,
+                                                             MaskPrep mp) {
   const int blk = blockIdx.x;
   if (blk < nv)
     vamax_rows<D, DT, true>(v, vsb, vss, vsh, Hkv, Skv, vchunks, vamax_chunk_rows(Skv), vpart, blk);
   else if (blk < nv + nk)
     quant_k_rows64<D, DT>(k, ksb, kss, ksh, Hkv, Skv, Skp, k8, ks, blk - nv);
-  else
+  else if (blk < nv + nk + nq)
     quant_q_rows<D, DT>(x, sb, ss, sh, H, Sq, row_tiles, qs_mul, q8, qs, blk - nv - nk);
+  else
+    mask_prep_block(mp, blk - nv - nk - nq);
 }
 
 // quant_kv (stage entry point): grid = (Skp / 128 * B * Hkv), block = 256; K then V of 128 keys
@@ -417,13 +432,18 @@ __global__ __launch_bounds__(256) void quant_kv_kernel(const uint16_t* __restric
   quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vs, 0, nullptr, v8t, blockIdx.x);
 }
 
-// sage_forward's second launch: V only, reducing the per-chunk maxima of the first
+// sage_forward's second launch: V (blocks [0, nvb)), reducing the per-chunk maxima of the first; then the mask
+// range blocks of sage_forward_masked (mp.range_blocks), which read the classes the first launch wrote
 template <int D, int DT>
 __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict__ v, int64_t vsb, int64_t vss,
                                                       int64_t vsh, int Hkv, int S, int Skp,
                                                       const float* __restrict__ vpart, int vchunks,
-                                                      float* __restrict__ vs, uint8_t* __restrict__ v8t) {
-  quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vpart, vchunks, vs, v8t, blockIdx.x);
+                                                      float* __restrict__ vs, uint8_t* __restrict__ v8t, int nvb,
+                                                      MaskPrep mp) {
+  if ((int)blockIdx.x < nvb)
+    quant_v_rows<D, DT>(v, vsb, vss, vsh, Hkv, S, Skp, vpart, vchunks, vs, v8t, blockIdx.x);
+  else
+    mask_range_block(mp, blockIdx.x - nvb);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -543,18 +563,20 @@ template <int D, int DT>
 static void launch_forward_quant(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb,
                                  int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, int B,
                                  int H, int Hkv, int Sq, int Skv, float qs_mul, int8_t* q8, float* qs, float* vpart,
-                                 int8_t* k8, float* ks, uint8_t* v8t, float* vs, hipStream_t st) {
+                                 int8_t* k8, float* ks, uint8_t* v8t, float* vs, const MaskPrep& mp, hipStream_t st) {
   const int tiles = (Sq + 63) / 64;
   const int Skp = kv_pad(Skv);
   const int vchunks = vamax_chunks(Skv);
   const int nv = vchunks * B * Hkv;
   const int nk = Skp / 64 * B * Hkv;
-  hipLaunchKernelGGL((quant_qk_vamax_kernel<D, DT>), dim3(nv + nk + tiles * B * H), dim3(256), 0, st,
+  const int nq = tiles * B * H;
+  const int nvb = Skp / 128 * B * Hkv;
+  hipLaunchKernelGGL((quant_qk_vamax_kernel<D, DT>), dim3(nv + nk + nq + mp.prep_blocks), dim3(256), 0, st,
                      static_cast<const uint16_t*>(q), qsb, qss, qsh, H, Sq, tiles, qs_mul, q8, qs,
                      static_cast<const uint16_t*>(k), ksb, kss, ksh, Skp, nk, k8, ks,
-                     static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, vchunks, nv, vpart);
-  hipLaunchKernelGGL((quant_v_kernel<D, DT>), dim3(Skp / 128 * B * Hkv), dim3(256), 0, st,
-                     static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, Skp, vpart, vchunks, vs, v8t);
+                     static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, vchunks, nv, vpart, nq, mp);
+  hipLaunchKernelGGL((quant_v_kernel<D, DT>), dim3(nvb + mp.range_blocks), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(v), vsb, vss, vsh, Hkv, Skv, Skp, vpart, vchunks, vs, v8t, nvb, mp);
 }
 
 template <int D, int DT>
@@ -625,11 +647,12 @@ int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D) {
   return (int64_t)B * Hkv * vamax_chunks(Skv) * layout_dim(D) * (int64_t)sizeof(float);
 }
 
-// Validation of every argument is done by the caller (sage_forward) through the per-stage checks below.
+// Validation of every argument is done by the caller (sage_forward) through the per-stage checks below.  mp: the
+// mask work of sage_forward_masked (NULL: none), run as extra workgroups of the two launches.
 int forward_quant_impl(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                        int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, int B, int H, int Hkv, int Sq,
                        int Skv, int D, int dtype, float qs_mul, int8_t* q8, float* qs, float* vpart, int8_t* k8,
-                       float* ks, uint8_t* v8t, float* vs, void* stream) {
+                       float* ks, uint8_t* v8t, float* vs, const MaskPrep* mp, void* stream) {
   const char* who = "sage_forward";
   int rc = check_common(B, H, Sq, D, dtype, who);
   if (rc) return rc;
@@ -640,8 +663,9 @@ int forward_quant_impl(const void* q, int64_t qsb, int64_t qss, int64_t qsh, con
   SAGE_REQUIRE(q8 && qs && vpart && k8 && ks && v8t && vs, "%s: an intermediate pointer is NULL", who);
   SAGE_REQUIRE(aligned16(q8) && aligned16(k8) && aligned16(v8t) && aligned16(vpart) && aligned16(vs),
                "%s: q8 / k8 / v8t / vs / workspace must be 16-byte aligned", who);
+  const MaskPrep none{};
   SAGE_DISPATCH_D_DT(D, dtype, launch_forward_quant, q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv,
-                     Sq, Skv, qs_mul, q8, qs, vpart, k8, ks, v8t, vs, (hipStream_t)stream);
+                     Sq, Skv, qs_mul, q8, qs, vpart, k8, ks, v8t, vs, mp ? *mp : none, (hipStream_t)stream);
   return check_launch("quantization launch");
 }
 
