@@ -399,8 +399,12 @@ __device__ __forceinline__ void quant_v_rows(const uint16_t* __restrict__ v, int
 // sage_forward's first launch: blocks [0, nv) write per-chunk V maxima (vamax_chunk_rows keys each) to `vpart`,
 // blocks [nv, nv + nk) quantize 64 keys of K each, the next nq quantize Q, and sage_forward_masked's mask blocks
 // (mp.prep_blocks of them) follow.  The V blocks come first so their longer row loops start early.
+// waves per SIMD the first launch asks for: 5 fit the d128 paths in 96 VGPRs (more loads in flight per CU); d256
+// holds twice the row slice and stays at the register count it needs
+template <int D> constexpr int quant_qk_waves() { return D == 256 ? 1 : 5; }
+
 template <int D, int DT>
-__global__ __launch_bounds__(256) void quant_qk_vamax_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
+__global__ __launch_bounds__(256, quant_qk_waves<D>()) void quant_qk_vamax_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t ss,
                                                              int64_t sh, int H, int Sq, int row_tiles, float qs_mul,
                                                              int8_t* __restrict__ q8, float* __restrict__ qs,
                                                              const uint16_t* __restrict__ k, int64_t ksb, int64_t kss,
