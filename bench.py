@@ -238,6 +238,32 @@ def main():
     torch.cuda.synchronize()
     ms_sdpa = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    # ---- a boolean key-padding mask (the last eighth of the keys hidden): the masked call, timed like the step, and
+    # torch SDPA bf16 with the same mask (non-causal configurations) ----
+    masked = None
+    if not cfg.causal:
+        mask = (torch.arange(S, device=dev) < S - S // 8)[None, None, None, :].expand(B, 1, 1, S)
+
+        def wall(fn, n):
+            for _ in range(min(args.warmup, 50)):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(n):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / n
+
+        if routed:
+            mfn = lambda: sageattention.sageattn(q, k, v, tensor_layout="HND", attn_mask=mask)  # noqa: E731
+        else:
+            mfn = lambda: cdna4_sage.attention(q, k, v, "HND", attn_mask=mask)  # noqa: E731
+        ms_mask = wall(mfn, args.steps)
+        ms_mask_sdpa = wall(lambda: F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=Hkv != H),
+                            max(10, args.steps // 10))
+        masked = {"mask": f"bool [B, 1, 1, S], first {S - S // 8} of {S} keys visible", "ms": round(ms_mask, 4),
+                  "sdpa_bf16_ms": round(ms_mask_sdpa, 4), "speedup_vs_sdpa_bf16": round(ms_mask_sdpa / ms_mask, 3)}
+
     traffic, traffic_src = profiled_traffic(args.config)
     result = {
         "metric": "attention TOPS + ms/call (Flux 24x4608x128), % of int8/fp8 MFMA peak",
@@ -274,6 +300,8 @@ def main():
             "device": torch.cuda.get_device_name(dev),
         },
     }
+    if masked is not None:
+        result["detail"]["key_padding_mask"] = masked
     if t_attn_whole is not None:
         result["detail"]["kernel_ms"]["attn_without_split"] = round(t_attn_whole, 5)
     if cfg.return_lse:

@@ -171,7 +171,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
   }
 
   // ---- mask: this lane's bit row and this wave's class row; the workgroup runs only the tiles from the first to the
-  // last that any of its rows sees (mask_range_kernel; the tiles outside hold no visible key, so skipping them is
+  // last that any of its rows sees (mask_range_block; the tiles outside hold no visible key, so skipping them is
   // exactly the online softmax over them) ----
   const uint8_t* mbase = nullptr;  // this (batch, head)'s mask words; the lane's row at byte offset moff
   uint32_t moff = 0;                 // (a (batch, head) slice of the bits is below 2 GiB, checked on the host)

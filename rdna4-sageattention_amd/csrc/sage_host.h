@@ -42,7 +42,8 @@ __host__ __device__ constexpr int layout_dim(int d) { return d == 96 ? 128 : d; 
 // padded KV length used by every K8 / KS / V8T layout
 inline int kv_pad(int skv) { return (skv + SAGE_KV_PAD - 1) / SAGE_KV_PAD * SAGE_KV_PAD; }
 
-// Boolean attention mask as the attention kernel reads it (built by mask_prep_kernel and mask_range_kernel).
+// Boolean attention mask as the attention kernel reads it (built by mask_prep_block and mask_range_block of
+// sage_mask.h, inside the two quantization launches).
 // bits: one 32-bit word per (row, 64-key tile, lane half hf): bit 16 kb + v is the visibility of the key that the QK
 // accumulator gives lane (query, hf) in register v of 32-key block kb, i.e. key 64 t + 32 kb + 8 (v / 4) + 4 hf + v % 4.
 // cls: per (32-row group, tile) 0 = no row sees a key of the tile, 1 = every row sees every key, 2 = mixed.  range:

@@ -119,6 +119,26 @@ def test_all_true_mask_is_the_unmasked_kernel(dev):
         assert torch.equal(cdna4_sage.attention(q, k, v, attn_mask=m.to(dev)), base)
 
 
+def test_flux_size_identities(dev):
+    """Config 2 (Flux 1x24x4608x128) at full size, by size-independent properties: an all-True mask is the unmasked
+    call bit for bit (whole and split tiles of the plan), and a key-padding mask that hides the last 512 keys equals
+    the call whose padding mask is the kv_len bound, i.e. every output row differs from the unmasked call and none is
+    NaN; a mask hiding everything gives zeros."""
+    from cdna4_sage.configs import CONFIGS, make_inputs
+    cfg = CONFIGS["2"]
+    q, k, v = (t.to(dev) for t in make_inputs(cfg))
+    base = cdna4_sage.attention(q, k, v)
+    S = cfg.S
+    assert torch.equal(cdna4_sage.attention(q, k, v, attn_mask=torch.ones(S, dtype=torch.bool, device=dev)), base)
+    pad = torch.arange(S, device=dev) < S - 512
+    out = cdna4_sage.attention(q, k, v, attn_mask=pad)
+    assert torch.isfinite(out).all() and not torch.equal(out, base)
+    ref = F.scaled_dot_product_attention(q[:, :2].float(), k[:, :2].float(), v[:, :2].float(), attn_mask=pad)
+    assert cosine(out[:, :2].float().cpu().numpy(), ref.cpu().numpy()) >= COS
+    none = cdna4_sage.attention(q, k, v, attn_mask=torch.zeros(S, dtype=torch.bool, device=dev))
+    assert (none == 0).all()
+
+
 def test_fully_masked_rows_and_tiles_give_zero(dev):
     q, k, v = (t.to(dev) for t in _inputs(2, 2, 2, 300, 600, 64, torch.float16, "HND", seed=6))
     none = torch.zeros(2, 1, 1, 600, dtype=torch.bool, device=dev)
