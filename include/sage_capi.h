@@ -19,7 +19,7 @@
  *    D = 96 is not rotated (kernel_build/build_kernels.py:36-37, sage_quant.py:18-30).
  *
  * Intermediate layouts (device memory, all contiguous; DL = sage_layout_dim(D): D, or 128 for D = 96 whose rows are
- * zero-padded so that the 128-channel attention kernel runs them):
+ * zero-padded; the attention kernel reads them as 128-channel tiles):
  *  - Q8  int8  [B, H, Sq, DL]             (head-major; the reference writes [B, Sq, H, D])
  *  - QS  fp32  [B, H, Sq]                 per-token scale / RB (D = 96: the scale itself), times the sm_scale fold
  *  - K8  int8  [B, Hkv, Skp, DL]          Skp = sage_kv_pad(Skv); rows >= Skv are zero

@@ -77,11 +77,13 @@ struct VarlenTiles {
 };
 
 
-// D is the channel count of the Q8 / K8 / V8T layouts; `dout` output channels are written (96 for head_dim 96, whose
-// layouts are zero-padded to 128; D otherwise).  c0 = log2(e) / sqrt(head_dim).
+// HD is the head dim; D = layout_dim(HD) the channel count of the Q8 / K8 / V8T layouts (128 for head_dim 96, whose
+// rows are zero-padded) and DA = HD the channels the MFMAs cover: the zero channels of head_dim 96 add nothing to S
+// and give output channels that are not written, so its tiles run 3 of the 4 QK and PV MFMA blocks of the 128-channel
+// layout.  `dout` output channels are written.  c0 = log2(e) / sqrt(head_dim).
 // MASK: a boolean mask (MaskTabs) instead of the causal / padding bound; the causal flag is folded into its bits.
-template <int D, bool CAUSAL, int OUT_DT, bool VARLEN, bool MASK = false>
-__global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
+template <int HD, bool CAUSAL, int OUT_DT, bool VARLEN, bool MASK = false>
+__global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void attn_kernel(
     const int8_t* __restrict__ q8, const float* __restrict__ qs, const int8_t* __restrict__ k8,
     const float* __restrict__ ks, const uint8_t* __restrict__ v8t, const float* __restrict__ vs,
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
@@ -89,12 +91,14 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<D>()) void attn_kernel(
     float c0, int dout, VarlenTiles vt, MaskTabs mt, const uint32_t* __restrict__ mbits_tab,
     const int* __restrict__ mcls_tab, const int2* __restrict__ mrange_tab) {
   static_assert(!(MASK && (CAUSAL || VARLEN)), "the mask variant folds causality into its bits and is dense only");
+  constexpr int D = layout_dim(HD);
+  constexpr int DA = HD;
   constexpr int BN = ATT_BN;
   constexpr int KTILE = BN * D;      // bytes of the K tile  ([64 keys][D], 16-byte chunks XOR-swizzled per row)
   constexpr int VTILE = D * BN;      // bytes of the V tile  ([D channels][64 keys])
   constexpr int TILE = KTILE + VTILE;
-  constexpr int NQK = D / 32;        // i8 MFMAs (K = 32 dims) per 32-key block
-  constexpr int NPV = D / 32;        // fp8 MFMAs (M = 32 channels) per tile
+  constexpr int NQK = DA / 32;       // i8 MFMAs (K = 32 dims) per 32-key block
+  constexpr int NPV = DA / 32;       // fp8 MFMAs (M = 32 channels) per tile
   constexpr int KCH = D / 16;        // 16-byte chunks per K row
   constexpr int KLOADS = KTILE / 1024 / 4;  // 1 KiB direct loads per wave per tile (4 waves)
   constexpr int VLOADS = VTILE / 1024 / 4;
@@ -538,12 +542,13 @@ static int device_cus(int* cus) {
   return SAGE_OK;
 }
 
-template <int D, bool CAUSAL, int OUT_DT>
+// HD: head dim (the kernel's template argument; its layouts have layout_dim(HD) channels)
+template <int HD, bool CAUSAL, int OUT_DT>
 static int resident_blocks(int* per_cu) {
   static int cache = 0;
   if (cache == 0) {
     int n = 0;
-    SAGE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<D, CAUSAL, OUT_DT, false>, ATT_THREADS, 0),
+    SAGE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_kernel<HD, CAUSAL, OUT_DT, false>, ATT_THREADS, 0),
                    "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     cache = n;
   }
@@ -551,8 +556,9 @@ static int resident_blocks(int* per_cu) {
   return SAGE_OK;
 }
 
-template <int D, bool CAUSAL, int OUT_DT>
+template <int HD, bool CAUSAL, int OUT_DT>
 static int make_plan(int B, int H, int Sq, int Skv, AttnPlan* p) {
+  constexpr int D = layout_dim(HD);
   const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
   p->n_tiles = B * H * q_tiles;
   p->n_full = p->n_tiles;
@@ -561,7 +567,7 @@ static int make_plan(int B, int H, int Sq, int Skv, AttnPlan* p) {
   if (CAUSAL) return SAGE_OK;
   int cus = 0, per_cu = 0, rc;
   if ((rc = device_cus(&cus))) return rc;
-  if ((rc = resident_blocks<D, CAUSAL, OUT_DT>(&per_cu))) return rc;
+  if ((rc = resident_blocks<HD, CAUSAL, OUT_DT>(&per_cu))) return rc;
   const int slots = cus * per_cu;
   if (slots <= 0) return SAGE_OK;
   const int rem = p->n_tiles % slots;
@@ -578,11 +584,13 @@ static int make_plan(int B, int H, int Sq, int Skv, AttnPlan* p) {
 // c0 = log2(e) / sqrt(head_dim) with the kernel's built-in sm_scale (other scales are folded into QS)
 static float logit_scale_base(int head_dim) { return (float)((1.0 / __builtin_sqrt((double)head_dim)) * 1.4426950408889634); }
 
-// D: layout channels (64, 128 or 256); hd: head_dim (96 runs on the 128-channel layout)
-template <int D, bool CAUSAL, int OUT_DT>
+// HD: head dim (64, 96, 128, 256); D = layout_dim(HD) channels of the intermediates (96 runs on the 128-channel
+// layout); hd == HD, the output channels
+template <int HD, bool CAUSAL, int OUT_DT>
 static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
                        const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, float* lse, int B, int H,
                        int Hkv, int Sq, int Skv, int hd, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  constexpr int D = layout_dim(HD);
   AttnPlan p;
   int rc;
   if (workspace == nullptr) {
@@ -591,7 +599,7 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
     p.chunks = 1;
     p.workspace = 0;
   } else {
-    if ((rc = make_plan<D, CAUSAL, OUT_DT>(B, H, Sq, Skv, &p))) return rc;
+    if ((rc = make_plan<HD, CAUSAL, OUT_DT>(B, H, Sq, Skv, &p))) return rc;
     SAGE_REQUIRE(workspace_bytes >= p.workspace, "sage_attn_fwd: workspace of %lld bytes, the plan needs %lld",
                  (long long)workspace_bytes, (long long)p.workspace);
     SAGE_REQUIRE(((uintptr_t)workspace & 255u) == 0, "sage_attn_fwd: workspace must be 256-byte aligned");
@@ -602,7 +610,7 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
   const float c0 = logit_scale_base(hd);
   uint16_t* o = static_cast<uint16_t*>(out);
   float* part = static_cast<float*>(workspace);
-  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
+  hipLaunchKernelGGL((attn_kernel<HD, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
                      vs, o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks,
                      part, c0, hd, VarlenTiles{}, MaskTabs{}, nullptr, nullptr, nullptr);
   if (n_split > 0) {
@@ -624,14 +632,15 @@ static int check_attn_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int c
   return SAGE_OK;
 }
 
-// dispatch on the layout channels (head_dim 96 -> 128)
-#define SAGE_ATTN_DISPATCH_DL(DL, CAUSAL, BF, FN, ...)                                                          \
-  ((CAUSAL) ? ((BF) ? FN<DL, true, DT_BF16>(__VA_ARGS__) : FN<DL, true, DT_F16>(__VA_ARGS__))                  \
-            : ((BF) ? FN<DL, false, DT_BF16>(__VA_ARGS__) : FN<DL, false, DT_F16>(__VA_ARGS__)))
-#define SAGE_ATTN_DISPATCH(D, CAUSAL, BF, FN, ...)                                                              \
-  (layout_dim(D) == 64    ? SAGE_ATTN_DISPATCH_DL(64, CAUSAL, BF, FN, __VA_ARGS__)                              \
-   : layout_dim(D) == 128 ? SAGE_ATTN_DISPATCH_DL(128, CAUSAL, BF, FN, __VA_ARGS__)                             \
-                          : SAGE_ATTN_DISPATCH_DL(256, CAUSAL, BF, FN, __VA_ARGS__))
+// dispatch on the head dim (checked by the caller to be 64, 96, 128 or 256)
+#define SAGE_ATTN_DISPATCH_HD(HDV, CAUSAL, BF, FN, ...)                                                         \
+  ((CAUSAL) ? ((BF) ? FN<HDV, true, DT_BF16>(__VA_ARGS__) : FN<HDV, true, DT_F16>(__VA_ARGS__))                \
+            : ((BF) ? FN<HDV, false, DT_BF16>(__VA_ARGS__) : FN<HDV, false, DT_F16>(__VA_ARGS__)))
+#define SAGE_ATTN_DISPATCH(HD, CAUSAL, BF, FN, ...)                                                             \
+  ((HD) == 64    ? SAGE_ATTN_DISPATCH_HD(64, CAUSAL, BF, FN, __VA_ARGS__)                                       \
+   : (HD) == 96  ? SAGE_ATTN_DISPATCH_HD(96, CAUSAL, BF, FN, __VA_ARGS__)                                       \
+   : (HD) == 128 ? SAGE_ATTN_DISPATCH_HD(128, CAUSAL, BF, FN, __VA_ARGS__)                                      \
+                 : SAGE_ATTN_DISPATCH_HD(256, CAUSAL, BF, FN, __VA_ARGS__))
 
 int attn_plan_impl(int B, int H, int Sq, int Skv, int D, int causal, int* n_full, int* chunks, int64_t* ws) {
   int rc = check_attn_shape(B, H, H, Sq, Skv, D, causal, "sage_attn_plan");
@@ -666,11 +675,11 @@ int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* 
 
 namespace sage {
 
-template <int D, bool CAUSAL, int OUT_DT>
+template <int HD, bool CAUSAL, int OUT_DT>
 static int launch_attn_varlen(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks,
                               const uint8_t* v8t, const float* vs, void* out, int64_t oss, int64_t osh, int H, int Hkv,
                               int TQ, int TKP, int hd, int n_blocks, VarlenTiles vt, hipStream_t st) {
-  hipLaunchKernelGGL((attn_kernel<D, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
+  hipLaunchKernelGGL((attn_kernel<HD, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
                      v8t, vs, static_cast<uint16_t*>(out), (int64_t)0, oss, osh, nullptr, H, Hkv, TQ, 0, TKP, 0,
                      n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt, MaskTabs{}, nullptr, nullptr,
                      nullptr);
@@ -690,9 +699,9 @@ int attn_varlen_impl(const int8_t* q8, const float* qs, const int8_t* k8, const 
 // Masked attention (the mask variant of the kernel; validation by the caller, sage_forward_masked).  The plan is
 // the dense non-causal one (sage_attn_plan with causal = 0; the causal flag lives in the mask bits), so callers can
 // query it; the mask variant's occupancy is never below the dense kernel's.
-template <int D, bool CAUSAL, int OUT_DT>
+template <int HD, bool CAUSAL, int OUT_DT>
 static int plan_mask(int B, int H, int Sq, int Skv, AttnPlan* p) {
-  return make_plan<D, false, OUT_DT>(B, H, Sq, Skv, p);
+  return make_plan<HD, false, OUT_DT>(B, H, Sq, Skv, p);
 }
 
 int attn_mask_plan_impl(int B, int H, int Sq, int Skv, int D, int64_t* ws) {
@@ -703,20 +712,21 @@ int attn_mask_plan_impl(int B, int H, int Sq, int Skv, int D, int64_t* ws) {
   return SAGE_OK;
 }
 
-template <int D, bool CAUSAL, int OUT_DT>
+template <int HD, bool CAUSAL, int OUT_DT>
 static int launch_attn_mask(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
                             const float* vs, void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv,
                             int Sq, int Skv, int hd, MaskTabs mt, void* workspace, hipStream_t st) {
+  constexpr int D = layout_dim(HD);
   AttnPlan p;
   int rc;
-  if ((rc = plan_mask<D, false, OUT_DT>(B, H, Sq, Skv, &p))) return rc;
+  if ((rc = plan_mask<HD, false, OUT_DT>(B, H, Sq, Skv, &p))) return rc;
   const int q_tiles = (Sq + ATT_BM - 1) / ATT_BM;
   const int n_split = p.n_tiles - p.n_full;
   const int blocks = p.n_full + n_split * p.chunks;
   const float c0 = logit_scale_base(hd);
   uint16_t* o = static_cast<uint16_t*>(out);
   float* part = static_cast<float*>(workspace);
-  hipLaunchKernelGGL((attn_kernel<D, false, OUT_DT, false, true>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8,
+  hipLaunchKernelGGL((attn_kernel<HD, false, OUT_DT, false, true>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8,
                      ks, v8t, vs, o, osb, oss, osh, nullptr, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles,
                      p.n_full, p.chunks, part, c0, hd, VarlenTiles{}, mt, mt.bits, mt.cls, mt.range);
   if (n_split > 0) {

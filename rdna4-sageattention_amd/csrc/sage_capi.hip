@@ -67,7 +67,7 @@ const char* sage_manifest_json(void) {
          "\"attn\": {\"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"waves_per_simd\": {\"d64\": 3, \"d128\": 3, \"d256\": 2}, "
          "\"max_kv_chunks\": 16, "
          "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
-         "\"variants\": [\"d64\", \"d128\", \"d256\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
+         "\"variants\": [\"d64\", \"d96 (128-channel layout, 96 channels of MFMA work)\", \"d128\", \"d256\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
          "\"varlen\": {\"meta_threads\": 1024, \"sort_bins\": 2048, \"kv_rows_per_sequence\": \"multiple of 128\"}, "
          "\"mask\": {\"dtype\": \"bool\", \"broadcast\": [\"batch\", \"head\", \"row\"], \"causal\": \"folded into the bits\", "
          "\"tables\": [\"bits u32 per (row, 64-key tile, lane half)\", \"class per (32 rows, tile)\", \"tile range per 128 rows\"], "
