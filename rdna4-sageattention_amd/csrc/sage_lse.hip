@@ -84,18 +84,33 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
   // direct-load sources: load j of wave w fills LDS chunk L = (w * LOADS + j) * 64 + lane, which holds tile row
   // L / KCH, logical chunk lse_swz(row, L % KCH) (the swizzle is an involution)
   int lrow[LOADS], lchunk[LOADS];
+  uint32_t koff[LOADS];  // byte offset of the load inside a whole tile (64 * kss < 2^31, checked on the host)
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
     const int L = (wave * LOADS + j) * 64 + lane;
     lrow[j] = L / KCH;
     lchunk[j] = lse_swz<KCH>(lrow[j], L % KCH) * 8;  // in elements
+    koff[j] = (uint32_t)(((int64_t)lrow[j] * kss + lchunk[j]) * 2);
   }
+  // Whole tiles: the tile base pinned to an SGPR pair plus the lane's 32-bit offset (the saddr + voffset form, no
+  // per-load 64-bit address arithmetic).  The last tile, when partial, repeats the last key in its rows past Skv
+  // (masked below).
   auto issue = [&](int t, int buf) {
     uint8_t* dst = smem[buf];
+    if ((t + 1) * BN <= Skv) {
+      const uint8_t* kb = reinterpret_cast<const uint8_t*>(kbase + (int64_t)t * BN * kss);
+      asm volatile("" : "+s"(kb));
 #pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      const int key = min(t * BN + lrow[j], Skv - 1);  // rows past Skv repeat the last key (masked below)
-      lse_copy16(kbase + (int64_t)key * kss + lchunk[j], dst + (wave * LOADS + j) * 1024);
+      for (int j = 0; j < LOADS; ++j) {
+        asm volatile("" : "+v"(koff[j]));
+        lse_copy16(kb + koff[j], dst + (wave * LOADS + j) * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        const int key = min(t * BN + lrow[j], Skv - 1);
+        lse_copy16(kbase + (int64_t)key * kss + lchunk[j], dst + (wave * LOADS + j) * 1024);
+      }
     }
   };
 
@@ -150,7 +165,9 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
       for (int v = 0; v < 16; ++v) ps[v & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, neg));
     l = l * corr + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
     m = m_new;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // the wait for the next tile's direct loads comes after this tile's arithmetic (l is its last result; without
+    // the operand the scheduler may hoist the wait into the middle of the tile)
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(l) : : "memory");
     __syncthreads();
   }
   const float lt = l + xor32_f32(l);
