@@ -50,6 +50,7 @@ extern "C" {
 
 #define SAGE_DTYPE_BF16 0
 #define SAGE_DTYPE_F16 1
+#define SAGE_DTYPE_BOOL 2 /* attention masks only */
 
 #define SAGE_KV_BLOCK 32  /* keys per K scale (kernel_build/build_kernels.py:326) */
 #define SAGE_KV_PAD 128   /* K8 / V8T rows are padded to a multiple of this */
@@ -173,30 +174,33 @@ int sage_forward_varlen(const void* q, int64_t qss, int64_t qsh, const void* k, 
                         float* ks, uint8_t* v8t, float* vs, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * Boolean attention masks (torch SDPA's bool attn_mask: nonzero byte = the query attends the key).  The mask is
- * addressed as mask + b*msb + h*msh + i*msq + j for batch b, query head h, query i, key j (byte strides; the key axis
- * is contiguous; a stride of 0 broadcasts that axis, as torch's expand gives).  No counterpart in the reference:
- * src/rdna4_sage/__init__.py:78-79 sends every masked call to torch SDPA (`attn_mask is not None` -> `_sdpa`).
+ * Attention masks with torch SDPA's semantics: mask_dtype SAGE_DTYPE_BOOL (a nonzero byte = the query attends the
+ * key) or an additive float mask of the inputs' dtype (SAGE_DTYPE_BF16 / SAGE_DTYPE_F16: added to the scaled scores,
+ * -inf = masked).  The mask is addressed as mask + b*msb + h*msh + i*msq + j (in elements) for batch b, query head h,
+ * query i, key j; the key axis is contiguous and a stride of 0 broadcasts that axis, as torch's expand gives.  No
+ * counterpart in the reference: src/rdna4_sage/__init__.py:78-79 sends every masked call to torch SDPA
+ * (`attn_mask is not None` -> `_sdpa`).
  *
  * sage_mask_workspace: bytes of the workspace sage_forward_masked needs for this shape and mask on the current device
- * (the attention's split state, the per-chunk V maxima and the mask's bit and class tables).
+ * (the attention's split state, the per-chunk V maxima and the mask's tables).
  */
-int sage_mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t msb, int64_t msh,
-                        int64_t msq, int64_t* workspace_bytes);
+int sage_mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int mask_dtype, int64_t msb,
+                        int64_t msh, int64_t msq, int64_t* workspace_bytes);
 
 /*
- * sage_forward with a boolean mask: the same quantization and quantized attention, with the scores of masked keys
- * at -inf (ANDed with the bottom-right causal mask when causal is set).  A query row that sees no key is written as 0
- * (torch SDPA gives NaN there).  Same arguments as sage_forward plus the mask; workspace: sage_mask_workspace bytes,
- * 256-byte aligned (required).  Replaces, for bool masks, the torch SDPA call of src/rdna4_sage/__init__.py:44-56
- * (`_sdpa`) that the reference makes for every call with an attn_mask.
+ * sage_forward with an attention mask: the same quantization and quantized attention, with the mask applied to the
+ * scores (bool: masked keys at -inf; float: the values added, ANDed / combined with the bottom-right causal mask when
+ * causal is set).  A query row that sees no key is written as 0 (torch SDPA gives NaN there).  Same arguments as
+ * sage_forward plus the mask; workspace: sage_mask_workspace bytes, 256-byte aligned (required).  Replaces, for
+ * these masks, the torch SDPA call of src/rdna4_sage/__init__.py:44-56 (`_sdpa`) that the reference makes for every
+ * call with an attn_mask.
  */
 int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                         int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb,
                         int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal,
-                        float qs_mul, const void* mask, int64_t msb, int64_t msh, int64_t msq, int8_t* q8, float* qs,
-                        int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace, int64_t workspace_bytes,
-                        void* stream);
+                        float qs_mul, const void* mask, int mask_dtype, int64_t msb, int64_t msh, int64_t msq,
+                        int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,7 +39,10 @@ What each function restates (paths relative to the reference checkout):
                         -inf like the causal mask.  The reference sends every masked call to torch SDPA
                         (src/rdna4_sage/__init__.py:78-79); the quantized masked math here is this build's own
                         definition, pinned by the all-True, causal-equivalent and padding-equivalent identities
-                        in tests/test_oracle.py and by the float64 masked softmax ``sdpa_reference``.
+                        in tests/test_oracle.py and by the float64 masked softmax ``sdpa_reference``.  A float
+                        ``attn_mask`` is additive (SDPA's convention); the kernel's bias path (``_bias_tile``) is
+                        pinned by the all-zero (= no mask), {0, -inf} (= the boolean mask) and per-row-constant
+                        (softmax shift invariance) identities and by float64 attention with the same bias.
 * ``sage_forward_varlen`` src/sageattention/core.py:66-89 (`sageattn_varlen`): one ``sage_forward`` per sequence
                         of the packed batch.
 * ``lse_reference``     src/sageattention/core.py:36-57 (`_lse`).
@@ -265,7 +268,10 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
 
     ``attn_mask``: bool array broadcastable to [B, H, Sq, seq_kv], True where the query attends the key (the
     convention of torch SDPA's boolean masks; no counterpart in the reference's kernel, which sends masked calls to
-    SDPA).  Masked scores are -inf like the causal ones, ANDed with the causal mask when both are given."""
+    SDPA).  Masked scores are -inf like the causal ones, ANDed with the causal mask when both are given.  A float
+    array is an additive mask (SDPA: softmax(Q K^T * scale + mask), -inf = masked), emulated as the gfx950 kernel
+    runs it: per 32-row group (a wave) and key tile whose values are all 0 or -inf, the boolean path above; otherwise
+    the bias path of ``_online_softmax``."""
     B, H, Sq, D = q8.shape
     Hkv = k8.shape[1]
     assert block_n % KV_BLOCK == 0 and H % Hkv == 0
@@ -274,7 +280,11 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     cl = (logit_scale_base(D) * qs.astype(F32)).astype(F32)      # [B, H, Sq]
     n_tiles = (seq_kv + block_n - 1) // block_n
     if attn_mask is not None:
-        attn_mask = np.broadcast_to(np.asarray(attn_mask, dtype=bool), (B, H, q8.shape[2], seq_kv))
+        attn_mask = np.asarray(attn_mask)
+        if attn_mask.dtype == bool:
+            attn_mask = np.broadcast_to(attn_mask, (B, H, q8.shape[2], seq_kv))
+        else:
+            attn_mask = np.broadcast_to(attn_mask.astype(F32), (B, H, q8.shape[2], seq_kv))
     o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask)
     if kv_split is not None:
         chunks, rows = kv_split
@@ -310,7 +320,11 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
 
 def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi, attn_mask=None):
     """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row.  attn_mask:
-    None or bool [B, H, Sq, seq_kv], True = attend."""
+    None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).
+
+    Bias path (float masks, tiles of a 32-row group holding a value other than 0 and -inf), in log2 units:
+    t = fma(F, ct, fma(b, log2e, -fp32(1.5 * 2^23 * ct))) per score, the tile's row max of t against m * cl for the
+    lazy rescale (m_new = m_cand * fp32(1 / cl) when it moves), p = exp2(t - cl * m_ref)."""
     B, H, Sq, D = q8.shape
     Hkv, Sp = k8.shape[1], k8.shape[2]
     hk = np.arange(H) // (H // Hkv)
@@ -336,11 +350,24 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
         mask = cols[None, :] >= seq_kv
         if causal:
             mask = mask | (cols[None, :] > rows[:, None] + causal_off)
+        bias_rows = None
         if attn_mask is not None:
-            am = np.zeros((B, H, Sq, block_n), dtype=bool)
             nv = max(0, min(j0 + block_n, seq_kv) - j0)
-            am[..., :nv] = attn_mask[..., j0:j0 + nv]
-            mask = mask | ~am
+            if attn_mask.dtype == bool:
+                am = np.zeros((B, H, Sq, block_n), dtype=bool)
+                am[..., :nv] = attn_mask[..., j0:j0 + nv]
+                mask = mask | ~am
+            else:
+                bt = np.full((B, H, Sq, block_n), -np.inf, dtype=F32)
+                bt[..., :nv] = attn_mask[..., j0:j0 + nv]
+                bt = np.where(mask, F32(-np.inf), bt).astype(F32)
+                general = (bt != 0) & (bt != -np.inf)
+                ng = (Sq + 31) // 32
+                grp = np.zeros((B, H, ng), dtype=bool)
+                for g in range(ng):
+                    grp[:, :, g] = general[:, :, 32 * g:32 * g + 32].any(axis=(-1, -2))
+                bias_rows = grp[:, :, rows // 32]                          # [B, H, Sq]: this tile takes the bias path
+                mask = mask | (bt == -np.inf)
         s = np.where(mask, F32(-np.inf), s).astype(F32)
         kst = np.ones((B, Hkv, nsub), dtype=F32)
         nb = min(nsub, ks.shape[2] - j0 // KV_BLOCK)
@@ -368,6 +395,8 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
         fs = (sb + F32(SEED)).astype(F32)
         arg = (fs.astype(np.float64) * ct[..., None].astype(np.float64) + nk[..., None].astype(np.float64)).astype(F32)
         p = np.exp2(arg).astype(F32).reshape(B, H, Sq, block_n)
+        if bias_rows is not None and bias_rows.any():
+            p, corr, need, m_new = _bias_tile(fs, ct, bt, m, cl, threshold, bias_rows, p, corr, need, m_new)
         tile_sum = p.sum(axis=-1, dtype=F32)
         l = ((corr * l).astype(F32) + tile_sum).astype(F32)
         o = np.where(need[..., None], (o * corr[..., None]).astype(F32), o)
@@ -375,6 +404,34 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
         o = (o + np.matmul(p8, vt[:, hk])).astype(F32)
         m = m_new
     return o, m, l
+
+
+def _bias_tile(fs, ct, bt, m, cl, threshold, rows, p, corr, need, m_new):
+    """The bias path of one tile for the rows in `rows` (other rows keep p, corr, need, m_new as given).  fs: the
+    seeded scores [B, H, Sq, nsub, 32]; ct [B, H, Sq, nsub]; bt: the additive mask of the tile [B, H, Sq, block_n]."""
+    B, H, Sq = m.shape
+    nsub = ct.shape[-1]
+    f64 = np.float64
+    bb = bt.reshape(B, H, Sq, nsub, KV_BLOCK)
+    nseed = -(F32(SEED) * ct).astype(F32)                                 # -fp32(1.5 * 2^23 * ct)
+    with np.errstate(invalid="ignore", over="ignore"):
+        inner = (bb.astype(f64) * f64(F32(LOG2E)) + nseed[..., None].astype(f64)).astype(F32)
+        t = (fs.astype(f64) * ct[..., None].astype(f64) + inner.astype(f64)).astype(F32)
+    t = t.reshape(B, H, Sq, -1)
+    rowmax = t.max(axis=-1)
+    with np.errstate(invalid="ignore"):
+        mc = (m * cl).astype(F32)
+        mcand = np.maximum(mc, rowmax).astype(F32)
+        nd = (mcand - mc).astype(F32) > F32(threshold)
+    rcl = (F32(1.0) / cl).astype(F32)
+    mn = np.where(nd, (mcand * rcl).astype(F32), m).astype(F32)
+    mref = np.where(mn == -np.inf, F32(0.0), mn).astype(F32)
+    with np.errstate(invalid="ignore"):
+        cr = np.exp2(((m - mref).astype(F32) * cl).astype(F32)).astype(F32)
+    negl = (F32(0.0) - (cl * mref).astype(F32)).astype(F32)
+    pb = np.exp2((t + negl[..., None]).astype(F32)).astype(F32)
+    return (np.where(rows[..., None], pb, p), np.where(rows, cr, corr), np.where(rows, nd, need),
+            np.where(rows, mn, m_new).astype(F32))
 
 
 def split_rows(B: int, H_total: int, Sq: int, n_full: int, heads=None, block_m: int = 128) -> np.ndarray:
@@ -429,8 +486,8 @@ def sage_forward_varlen(q, k, v, cu_q, cu_k, causal=False, sm_scale=None, block_
 # Textbook references used to bound the emulation
 # ----------------------------------------------------------------------------------------------------------
 def sdpa_reference(q, k, v, causal=False, sm_scale=None, attn_mask=None):
-    """float64 softmax attention, bottom-right causal, GQA by head repetition; attn_mask: bool, broadcastable to
-    [B, H, Sq, Skv], True = attend.  A row that sees no key is 0."""
+    """float64 softmax attention, bottom-right causal, GQA by head repetition; attn_mask: bool (True = attend) or float
+    (added to the scaled scores), broadcastable to [B, H, Sq, Skv].  A row that sees no key is 0."""
     B, H, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
     rep = H // Hkv
@@ -442,7 +499,11 @@ def sdpa_reference(q, k, v, causal=False, sm_scale=None, attn_mask=None):
         mask = np.arange(Skv)[None, :] > np.arange(Sq)[:, None] + (Skv - Sq)
         s = np.where(mask, -np.inf, s)
     if attn_mask is not None:
-        s = np.where(np.broadcast_to(np.asarray(attn_mask, dtype=bool), s.shape), s, -np.inf)
+        am = np.asarray(attn_mask)
+        if am.dtype == bool:
+            s = np.where(np.broadcast_to(am, s.shape), s, -np.inf)
+        else:
+            s = s + np.broadcast_to(am.astype(np.float64), s.shape)
     mx = s.max(axis=-1, keepdims=True)
     seen = np.isfinite(mx)
     p = np.exp(s - np.where(seen, mx, 0.0))

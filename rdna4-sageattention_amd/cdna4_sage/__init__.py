@@ -6,10 +6,11 @@ libsage_capi.so and launched through its C ABI on torch's current stream.
     import cdna4_sage
     out = cdna4_sage.sageattn(q, k, v, tensor_layout="HND")   # drop-in for sageattention.sageattn
 
-Routing mirrors the reference's src/rdna4_sage/__init__.py:20-84: small problems, unsupported shapes or GPUs,
-float (additive) masks and causal calls with q_len > kv_len go to torch's SDPA binding; everything else runs the
-gfx950 kernels, including two cases the reference sends to SDPA: causal calls with q_len < kv_len (bottom-right
-aligned) and boolean attn_masks (set CDNA4_SAGE_NATIVE_MASK=0 to send masks to SDPA as the reference does).
+Routing mirrors the reference's src/rdna4_sage/__init__.py:20-84: small problems, unsupported shapes or GPUs, masks
+of another dtype and causal calls with q_len > kv_len go to torch's SDPA binding; everything else runs the gfx950
+kernels, including two cases the reference sends to SDPA: causal calls with q_len < kv_len (bottom-right aligned) and
+attn_masks (bool, or additive of q's dtype; set CDNA4_SAGE_NATIVE_MASK=0 to send masks to SDPA as the reference
+does).
 attention_varlen runs packed variable-length batches in one pass.
 """
 import os
@@ -40,7 +41,8 @@ def _env_int(names, default):
 # CDNA4_SAGE_* take precedence; the reference's RDNA4_SAGE_* names are honoured for drop-in callers.
 MIN_WORK = _env_int(("CDNA4_SAGE_MIN_WORK", "RDNA4_SAGE_MIN_WORK"), 64 * 2**20)  # batch * heads * q_len * kv_len
 MIN_KV = _env_int(("CDNA4_SAGE_MIN_KV", "RDNA4_SAGE_MIN_KV"), 1024)
-# Boolean attn_masks run on the kernel (quantized like every other call); 0 restores the reference's SDPA routing.
+# attn_masks (bool, or additive of q's dtype) run on the kernel (quantized like every other call); 0 restores the
+# reference's SDPA routing.
 NATIVE_MASK = _env_int(("CDNA4_SAGE_NATIVE_MASK",), 1) != 0
 
 
@@ -54,8 +56,9 @@ def is_available(device=None) -> bool:
 
 def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False, attn_mask=None):
     """Run the int8/fp8 kernel; raises Unsupported if it cannot.  Output in the input layout and dtype.
-    Causal attention is bottom-right aligned and needs q_len <= kv_len.  attn_mask: None or a boolean mask (True =
-    attend) broadcastable to [B, H, q_len, kv_len]; a query row that sees no key is 0."""
+    Causal attention is bottom-right aligned and needs q_len <= kv_len.  attn_mask: None, a boolean mask (True =
+    attend) or an additive mask of q's dtype, broadcastable to [B, H, q_len, kv_len] as torch SDPA takes it; a query
+    row that sees no key is 0."""
     if attn_mask is None:
         out = ops.attention(q, k, v, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
     else:
@@ -94,9 +97,10 @@ def _worth_it(q, k, tensor_layout, is_causal=False):
 
 def sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, attn_mask=None, return_lse=False, **kwargs):
     """Drop-in for sageattention.sageattn.  Uses the gfx950 kernel when it applies and pays off, torch SDPA otherwise
-    (float masks, causal with q_len > kv_len, unsupported shapes or GPUs, small problems).  Causal attention is
-    bottom-right aligned as in SageAttention / FlashAttention.  A boolean attn_mask runs on the kernel (a query row
-    that sees no key gives 0 there, NaN in SDPA).  Extra SageAttention kwargs are ignored."""
+    (masks of another dtype, causal with q_len > kv_len, unsupported shapes or GPUs, small problems).  Causal attention
+    is bottom-right aligned as in SageAttention / FlashAttention.  A bool attn_mask, or an additive one of q's dtype,
+    runs on the kernel (a query row that sees no key gives 0 there, NaN in SDPA).  Extra SageAttention kwargs are
+    ignored."""
     if return_lse:
         raise NotImplementedError("cdna4_sage: return_lse is not supported here; use sageattention.sageattn")
     if (attn_mask is not None and not NATIVE_MASK) or not _worth_it(q, k, tensor_layout, is_causal):

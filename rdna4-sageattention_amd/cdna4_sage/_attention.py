@@ -95,12 +95,19 @@ def _shape(q, k, layout):
 
 
 def mask_view(attn_mask, q, k, layout):
-    """A boolean attn_mask (True = attend, broadcastable to [B, H, q_len, kv_len] as torch SDPA's) as the kernel reads
-    it: the mask expanded to [B, H, q_len, kv_len] with the key axis contiguous and broadcast axes at stride 0, and
-    its (batch, head, row) byte strides.  Only the key axis is ever materialised.  Raises Unsupported for float
-    masks (additive biases stay on SDPA) and for masks that do not broadcast."""
-    if not isinstance(attn_mask, torch.Tensor) or attn_mask.dtype != torch.bool:
-        raise Unsupported("only boolean attn_mask runs on the kernel (additive float masks go to SDPA)")
+    """An attn_mask with torch SDPA's semantics (bool: True = attend; a float mask of q's dtype: added to the scaled
+    scores, -inf = masked; broadcastable to [B, H, q_len, kv_len]) as the kernel reads it: the mask expanded to
+    [B, H, q_len, kv_len] with the key axis contiguous and broadcast axes at stride 0, its dtype code and its
+    (batch, head, row) element strides.  Only the key axis is ever materialised.  Raises Unsupported for other
+    dtypes and for masks that do not broadcast."""
+    if not isinstance(attn_mask, torch.Tensor):
+        raise Unsupported("attn_mask must be a tensor")
+    if attn_mask.dtype == torch.bool:
+        code = _capi.DTYPE_BOOL
+    elif attn_mask.dtype == q.dtype and attn_mask.dtype in DTYPES:
+        code = DTYPES[attn_mask.dtype]
+    else:
+        raise Unsupported(f"attn_mask dtype {attn_mask.dtype} (bool, or q's dtype {q.dtype} for an additive mask)")
     if attn_mask.device != q.device:
         raise Unsupported("attn_mask must be on the device of q")
     if attn_mask.dim() > 4:
@@ -113,17 +120,18 @@ def mask_view(attn_mask, q, k, layout):
     if Skv > 1 and m.stride(3) != 1:
         base = attn_mask.reshape((1,) * (4 - attn_mask.dim()) + tuple(attn_mask.shape))
         m = base.expand(*base.shape[:3], Skv).contiguous().expand(B, H, Sq, Skv)
-    return m, (m.stride(0), m.stride(1), m.stride(2))
+    return m, code, (m.stride(0), m.stride(1), m.stride(2))
 
 
 def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False, attn_mask=None):
-    """Attention, optionally causal (bottom-right aligned, q_len <= kv_len) and / or with a boolean attn_mask (True =
-    attend, broadcastable to [B, H, q_len, kv_len]; ANDed with the causal mask; a query row that sees no key is 0).
+    """Attention, optionally causal (bottom-right aligned, q_len <= kv_len) and / or with an attn_mask as torch SDPA
+    takes it (bool: True = attend; float of q's dtype: added to the scaled scores; broadcastable to
+    [B, H, q_len, kv_len]; combined with the causal mask; a query row that sees no key is 0).
     q: (B, H, Sq, D) for "HND" or (B, Sq, H, D) for "NHD"; k/v alike, with H a multiple of the kv head count.
     Returns (B, Sq, H, D) contiguous in q's dtype."""
     check_supported(q, k, v, layout, is_causal)
     if attn_mask is not None:
-        mask, mstr = mask_view(attn_mask, q, k, layout)
+        mask, mcode, mstr = mask_view(attn_mask, q, k, layout)
     dev = q.device
     if layout == "HND":
         B, H, Sq, D = q.shape
@@ -148,12 +156,12 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False, attn_mask=N
     out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
     di = dev.index if dev.index is not None else torch.cuda.current_device()
     if attn_mask is not None:
-        ws_bytes = _capi.mask_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal), *mstr)
+        ws_bytes = _capi.mask_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal), mcode, *mstr)
         ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
         with torch.cuda.device(dev):
             _capi.call("sage_forward_masked", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out),
                        *_out_strides(out), B, H, Hkv, Sq, Skv, D, dt, int(bool(is_causal)),
-                       qs_fold_factor(sm_scale, D), _ptr(mask), *mstr, _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks),
+                       qs_fold_factor(sm_scale, D), _ptr(mask), mcode, *mstr, _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks),
                        _ptr(v8t), _ptr(vs), _ptr(ws), ws_bytes, stream)
         return out
     ws_bytes = _capi.forward_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal))

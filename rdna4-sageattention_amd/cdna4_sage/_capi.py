@@ -18,8 +18,8 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 LIB_PATH = Path(__file__).resolve().parent / "libsage_capi.so"
 
 SAGE_OK, SAGE_ERR_INVALID, SAGE_ERR_UNSUPPORTED, SAGE_ERR_HIP = 0, 1, 2, 3
-DTYPE_BF16, DTYPE_F16 = 0, 1
-ABI_VERSION = 4
+DTYPE_BF16, DTYPE_F16, DTYPE_BOOL = 0, 1, 2
+ABI_VERSION = 5
 
 _lib = None
 _lock = threading.Lock()
@@ -47,9 +47,9 @@ SIGNATURES = {
     "sage_varlen_layout": ([_I, _I, _I, _I, _I, _P, _P], _I),
     "sage_forward_varlen": ([_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _P,
                              _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
-    "sage_mask_workspace": ([_I, _I, _I, _I, _I, _I, _I, _L, _L, _L, _P], _I),
+    "sage_mask_workspace": ([_I, _I, _I, _I, _I, _I, _I, _I, _L, _L, _L, _P], _I),
     "sage_forward_masked": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
-                             _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _L, _L, _L,
+                             _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _I, _L, _L, _L,
                              _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
 }
 
@@ -117,12 +117,12 @@ def forward_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv:
 
 
 @functools.lru_cache(maxsize=4096)
-def mask_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv: int, D: int, causal: bool, msb: int,
-                   msh: int, msq: int) -> int:
-    """Workspace bytes of sage_forward_masked for this shape and mask strides on device `device_index`."""
+def mask_workspace(device_index: int, B: int, H: int, Hkv: int, Sq: int, Skv: int, D: int, causal: bool,
+                   mask_dtype: int, msb: int, msh: int, msq: int) -> int:
+    """Workspace bytes of sage_forward_masked for this shape, mask dtype and mask strides on `device_index`."""
     ws = ctypes.c_int64()
     with torch.cuda.device(device_index):
-        call("sage_mask_workspace", B, H, Hkv, Sq, Skv, D, int(causal), msb, msh, msq, ctypes.byref(ws))
+        call("sage_mask_workspace", B, H, Hkv, Sq, Skv, D, int(causal), mask_dtype, msb, msh, msq, ctypes.byref(ws))
     return ws.value
 
 

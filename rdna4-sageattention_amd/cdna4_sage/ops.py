@@ -30,8 +30,9 @@ attention.register_fake(_fake)
 @torch.library.custom_op("cdna4_sage::attention_masked", mutates_args=())
 def attention_masked(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn_mask: torch.Tensor, layout: str,
                      sm_scale: float, is_causal: bool) -> torch.Tensor:
-    """attention with a boolean attn_mask (True = attend, broadcastable to [B, H, q_len, kv_len]); no counterpart in
-    the reference, which sends masked calls to SDPA.  Returns (B, Sq, H, D) contiguous."""
+    """attention with an attn_mask as torch SDPA takes it (bool True = attend, or additive of q's dtype; broadcastable
+    to [B, H, q_len, kv_len]); no counterpart in the reference, which sends masked calls to SDPA.  Returns
+    (B, Sq, H, D) contiguous."""
     return _attention.attention(q, k, v, layout, sm_scale if sm_scale > 0 else None, is_causal, attn_mask=attn_mask)
 
 

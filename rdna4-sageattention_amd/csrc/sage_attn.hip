@@ -58,6 +58,19 @@ __device__ __forceinline__ uint32_t load_global_u32(const uint8_t* p) {
   return *(const __attribute__((address_space(1))) uint32_t*)(p);
 }
 
+// 16 bytes through the global address space
+__device__ __forceinline__ v4i load_global_v4i(const uint8_t* p) {
+  return *(const __attribute__((address_space(1))) v4i*)(p);
+}
+
+// an additive mask element (the input dtype's 16 bits in the low half) as fp32
+template <int DT> __device__ __forceinline__ float mask_half_to_f32(uint32_t h) {
+  if constexpr (DT == DT_BF16)
+    return __uint_as_float(h << 16);
+  else
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
 constexpr int ATT_MAX_CHUNKS = 16;
 
 // Workspace of a split launch (units = split tiles x chunks): each chunk's O normalised by its own l, as fp16
@@ -89,7 +102,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     uint16_t* __restrict__ out, int64_t osb, int64_t oss, int64_t osh, float* __restrict__ lse, int H, int Hkv,
     int Sq_arg, int Skv_arg, int Skp, int q_tiles, int total, int n_full, int chunks, float* __restrict__ part,
     float c0, int dout, VarlenTiles vt, MaskTabs mt, const uint32_t* __restrict__ mbits_tab,
-    const int* __restrict__ mcls_tab, const int2* __restrict__ mrange_tab) {
+    const int* __restrict__ mcls_tab, const int2* __restrict__ mrange_tab, const uint16_t* __restrict__ mbias_tab) {
   static_assert(!(MASK && (CAUSAL || VARLEN)), "the mask variant folds causality into its bits and is dense only");
   constexpr int D = layout_dim(HD);
   constexpr int DA = HD;
@@ -162,6 +175,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     for (int i = 0; i < NQK; ++i) qa[i] = *reinterpret_cast<const v4i*>(qp + 32 * i);
   }
   const float cl = c0 * qs[qrow0 + qr];
+  const float rcl = 1.0f / cl;  // the bias tiles keep m in S * ks units
 
   // ---- KV range ----
   int kv_end = Skv;
@@ -179,10 +193,15 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   // exactly the online softmax over them) ----
   const uint8_t* mbase = nullptr;  // this (batch, head)'s mask words; the lane's row at byte offset moff
   uint32_t moff = 0;                 // (a (batch, head) slice of the bits is below 2 GiB, checked on the host)
+  const uint8_t* bbase = nullptr;  // the same for the bias values of an additive mask (64 bytes per word)
+  uint32_t boff = 0;
   const int* mcls = nullptr;
   if (MASK) {
-    mbase = reinterpret_cast<const uint8_t*>(mbits_tab + (int64_t)b * mt.bsb + (int64_t)h * mt.bsh);
+    const int64_t wslice = (int64_t)b * mt.bsb + (int64_t)h * mt.bsh;
+    mbase = reinterpret_cast<const uint8_t*>(mbits_tab + wslice);
     moff = (uint32_t)(((int64_t)qr * mt.bsq + hf) * 4);
+    bbase = reinterpret_cast<const uint8_t*>(mbias_tab + wslice * 32);
+    boff = (uint32_t)(((int64_t)qr * mt.bsq + hf) * 64);
     mcls = mcls_tab + (int64_t)b * mt.csb + (int64_t)h * mt.csh + (int64_t)min(q0 >> 5, mt.groups - 1) * mt.csg;
     const int2 r = mrange_tab[(int64_t)b * mt.rsb + (int64_t)h * mt.rsh + min(qt, mt.rblocks - 1)];
     t_lo = max(t_lo, r.x);
@@ -243,11 +262,13 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
   float m = -INFINITY, l = 0.0f;
   v8i pb = {};  // E4M3 probabilities (B operand of the PV MFMA); each cvt rewrites one half, so no clearing
+  const v4i bw_none[4] = {};  // the bias argument of the tile bodies without an additive mask
 
   // One tile: S^T = K Q^T (int8 MFMA), online softmax with the reference's lazy rescale, O^T += V^T P^T (fp8 MFMA).
   // MODE 0: every key visible; 1: keys beyond the causal / padding bound masked; 2: keys whose bit of MW is clear
-  // masked (MW = the lane's mask word of the tile).
-#define SAGE_TILE(T, MODE, MW)                                                                             \
+  // masked (MW = the lane's mask word of the tile); 3: the additive mask values BW (the lane's 32 16-bit values,
+  // input dtype, -inf = masked) added in log2 units, with the row max taken over the biased logits.
+#define SAGE_TILE(T, MODE, MW, BW)                                                                         \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
     const uint8_t* kt_ = smem[t_ & 1];                                                                     \
@@ -279,35 +300,65 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           sf_[kb_][v_] = __int_as_float((__float_as_int(sf_[kb_][v_]) & keep_) | (int)(0xFF800000u & ~(uint32_t)keep_)); \
         }                                                                                                  \
     }                                                                                                      \
-    /* block maxima on the bit patterns: the scores are positive floats (1.5 * 2^23 + S) or -inf, whose int32   \
-       patterns order like the floats, and an integer max needs no NaN canonicalisation */                  \
-    int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                               \
-    _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                    \
-      mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                        \
-      mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                        \
-    }                                                                                                      \
-    const float mx0_ = __int_as_float(max(mi0_, xor32_i32(mi0_)));                                         \
-    const float mx1_ = __int_as_float(max(mi1_, xor32_i32(mi1_)));                                         \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
-    const float rowmax_ = fmaxf((mx0_ - SEED_F) * ks0_, (mx1_ - SEED_F) * ks1_);                           \
-    const float mcand_ = fmaxf(m, rowmax_);                                                                \
-    const bool need_ = (mcand_ - m) * cl > 8.0f;                                                           \
-    const float mnew_ = need_ ? mcand_ : m;                                                                \
-    /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets    \
-       from 0 instead of -inf keep corr and the exponents free of NaN */                                   \
-    const float mref_ = ((MODE) != 0 && mnew_ == -INFINITY) ? 0.0f : mnew_;                               \
-    const float corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                          \
-    const float neg_ = 0.0f - cl * mref_;                                                                  \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
-    const float nk0_ = neg_ - SEED_F * ct0_, nk1_ = neg_ - SEED_F * ct1_;                                  \
-    float psum_ = 0.0f;                                                                                    \
-    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
-      sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, nk0_));                         \
-      psum_ += sf_[0][v_];                                                                                 \
-    }                                                                                                      \
-    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
-      sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, nk1_));                         \
-      psum_ += sf_[1][v_];                                                                                 \
+    bool need_;                                                                                            \
+    float mnew_, corr_, psum_ = 0.0f;                                                                      \
+    if ((MODE) == 3) {                                                                                     \
+      /* t = fma(F, ct, fma(b, log2e, -fp32(1.5 * 2^23 * ct))): the biased logit in log2 units (b = -inf for   \
+         a masked key gives -inf); the lazy rescale compares its row max with m * cl and keeps m in S * ks     \
+         units (m_new = m_cand * (1 / cl)) */                                                               \
+      const float ns0_ = -(SEED_F * ct0_), ns1_ = -(SEED_F * ct1_);                                        \
+      float tm_ = -INFINITY;                                                                               \
+      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
+          const uint32_t bw_ = (BW)[(16 * kb_ + v_) >> 3][((16 * kb_ + v_) >> 1) & 3];                     \
+          const float b_ = mask_half_to_f32<OUT_DT>((v_ & 1) ? (bw_ >> 16) : (bw_ & 0xFFFFu));             \
+          const float in_ = __builtin_fmaf(b_, 1.44269504088896341f, kb_ ? ns1_ : ns0_);                   \
+          sf_[kb_][v_] = __builtin_fmaf(sf_[kb_][v_], kb_ ? ct1_ : ct0_, in_);                             \
+          tm_ = fmaxf(tm_, sf_[kb_][v_]);                                                                  \
+        }                                                                                                  \
+      tm_ = fmaxf(tm_, xor32_f32(tm_));                                                                    \
+      const float mc_ = m * cl;                                                                            \
+      const float mcand_ = fmaxf(mc_, tm_);                                                                \
+      need_ = (mcand_ - mc_) > 8.0f;                                                                       \
+      mnew_ = need_ ? mcand_ * rcl : m;                                                                    \
+      const float mref_ = mnew_ == -INFINITY ? 0.0f : mnew_;                                               \
+      corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                                    \
+      const float negl_ = 0.0f - cl * mref_;                                                               \
+      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
+          sf_[kb_][v_] = __builtin_amdgcn_exp2f(sf_[kb_][v_] + negl_);                                     \
+          psum_ += sf_[kb_][v_];                                                                           \
+        }                                                                                                  \
+    } else {                                                                                               \
+      /* block maxima on the bit patterns: the scores are positive floats (1.5 * 2^23 + S) or -inf, whose     \
+         int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */          \
+      int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                             \
+      _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                  \
+        mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                      \
+        mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                      \
+      }                                                                                                    \
+      const float mx0_ = __int_as_float(max(mi0_, xor32_i32(mi0_)));                                       \
+      const float mx1_ = __int_as_float(max(mi1_, xor32_i32(mi1_)));                                       \
+      const float rowmax_ = fmaxf((mx0_ - SEED_F) * ks0_, (mx1_ - SEED_F) * ks1_);                         \
+      const float mcand_ = fmaxf(m, rowmax_);                                                              \
+      need_ = (mcand_ - m) * cl > 8.0f;                                                                    \
+      mnew_ = need_ ? mcand_ : m;                                                                          \
+      /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets  \
+         from 0 instead of -inf keep corr and the exponents free of NaN */                                 \
+      const float mref_ = ((MODE) != 0 && mnew_ == -INFINITY) ? 0.0f : mnew_;                             \
+      corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                                    \
+      const float neg_ = 0.0f - cl * mref_;                                                                \
+      const float nk0_ = neg_ - SEED_F * ct0_, nk1_ = neg_ - SEED_F * ct1_;                                \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
+        sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, nk0_));                       \
+        psum_ += sf_[0][v_];                                                                               \
+      }                                                                                                    \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
+        sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, nk1_));                       \
+        psum_ += sf_[1][v_];                                                                               \
+      }                                                                                                    \
     }                                                                                                      \
     l = corr_ * l + psum_;                                                                                 \
     m = mnew_;                                                                                             \
@@ -352,17 +403,17 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     // the end-of-tile wait for the direct loads covers them and no wait inside a tile waits for the next tile.
     int c_nxt = t < t_hi ? mcls[t] : 0;
     while (t < t_hi) {
-      for (; t < t_hi && c_nxt != 2; ++t) {
+      for (; t < t_hi && c_nxt < 2; ++t) {
         const int c_cur = c_nxt;
         if (t + 1 < t_hi) {
           c_nxt = mcls[t + 1];
           SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
         }
-        if (c_cur == 1) SAGE_TILE(t, 0, 0u);
+        if (c_cur == 1) SAGE_TILE(t, 0, 0u, bw_none);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
-      if (t < t_hi) {  // a run of class 2 (its first word is waited for once)
+      if (t < t_hi && c_nxt == 2) {  // a run of class 2 (its first word is waited for once)
         const uint8_t* mb_ = mbase;
         asm volatile("" : "+s"(mb_));
         uint32_t mw_cur = load_global_u32(mb_ + (moff + 8u * (uint32_t)t));
@@ -376,24 +427,40 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
             c_nxt = mcls[t + 1];
             SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
           }
-          SAGE_TILE(t, 2, mw_cur);
+          SAGE_TILE(t, 2, mw_cur, bw_none);
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           asm volatile("" ::"v"(mw_nxt));
           __syncthreads();
           mw_cur = mw_nxt;
         }
       }
+      // a run of class 3 (additive mask): the lane's 64 bytes of bias values of the tile are loaded before the next
+      // tile's direct loads, which are always issued here (the last iteration reloads its own tile into the idle
+      // buffer), so the wait for the values counts the direct loads behind them and does not wait for them
+      for (; t < t_hi && c_nxt == 3; ++t) {
+        const uint8_t* bb_ = bbase;
+        asm volatile("" : "+s"(bb_));
+        v4i bias_w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bias_w[i] = load_global_v4i(bb_ + (boff + 128u * (uint32_t)t + 16u * i));
+        const int tn_ = min(t + 1, t_hi - 1);
+        c_nxt = mcls[tn_];
+        SAGE_ISSUE_TILE(tn_, (t + 1) & 1);
+        SAGE_TILE(t, 3, 0u, bias_w);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
     }
   } else {
     for (; t < t_mask; ++t) {
       if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
-      SAGE_TILE(t, 0, 0u);
+      SAGE_TILE(t, 0, 0u, bw_none);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     }
     for (; t < t_hi; ++t) {
       if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
-      SAGE_TILE(t, 1, 0u);
+      SAGE_TILE(t, 1, 0u, bw_none);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     }
@@ -612,7 +679,7 @@ static int launch_attn(const int8_t* q8, const float* qs, const int8_t* k8, cons
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL((attn_kernel<HD, CAUSAL, OUT_DT, false>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks, v8t,
                      vs, o, osb, oss, osh, lse, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles, p.n_full, p.chunks,
-                     part, c0, hd, VarlenTiles{}, MaskTabs{}, nullptr, nullptr, nullptr);
+                     part, c0, hd, VarlenTiles{}, MaskTabs{}, nullptr, nullptr, nullptr, nullptr);
   if (n_split > 0) {
     if ((rc = check_launch("attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,
@@ -682,7 +749,7 @@ static int launch_attn_varlen(const int8_t* q8, const float* qs, const int8_t* k
   hipLaunchKernelGGL((attn_kernel<HD, CAUSAL, OUT_DT, true>), dim3(n_blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8, ks,
                      v8t, vs, static_cast<uint16_t*>(out), (int64_t)0, oss, osh, nullptr, H, Hkv, TQ, 0, TKP, 0,
                      n_blocks, n_blocks, 1, nullptr, logit_scale_base(hd), hd, vt, MaskTabs{}, nullptr, nullptr,
-                     nullptr);
+                     nullptr, nullptr);
   return check_launch("varlen attention launch");
 }
 
@@ -728,7 +795,7 @@ static int launch_attn_mask(const int8_t* q8, const float* qs, const int8_t* k8,
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL((attn_kernel<HD, false, OUT_DT, false, true>), dim3(blocks), dim3(ATT_THREADS), 0, st, q8, qs, k8,
                      ks, v8t, vs, o, osb, oss, osh, nullptr, H, Hkv, Sq, Skv, kv_pad(Skv), q_tiles, p.n_tiles,
-                     p.n_full, p.chunks, part, c0, hd, VarlenTiles{}, mt, mt.bits, mt.cls, mt.range);
+                     p.n_full, p.chunks, part, c0, hd, VarlenTiles{}, mt, mt.bits, mt.cls, mt.range, mt.bias);
   if (n_split > 0) {
     if ((rc = check_launch("masked attention launch"))) return rc;
     hipLaunchKernelGGL((attn_merge_kernel<D, OUT_DT>), dim3(n_split * (ATT_BM * D / 4 / 256)), dim3(256), 0, st,

@@ -49,7 +49,7 @@ static int forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int 
 
 extern "C" {
 
-int sage_abi_version(void) { return 4; }
+int sage_abi_version(void) { return 5; }
 
 const char* sage_last_error(void) { return sage::g_err; }
 
@@ -69,8 +69,8 @@ const char* sage_manifest_json(void) {
          "\"mfma_qk\": \"v_mfma_i32_32x32x32_i8\", \"mfma_pv\": \"v_mfma_f32_32x32x64_f8f6f4\", "
          "\"variants\": [\"d64\", \"d96 (128-channel layout, 96 channels of MFMA work)\", \"d128\", \"d256\"], \"causal\": true, \"gqa\": true, \"out_dtypes\": [\"bf16\", \"f16\"]}, "
          "\"varlen\": {\"meta_threads\": 1024, \"sort_bins\": 2048, \"kv_rows_per_sequence\": \"multiple of 128\"}, "
-         "\"mask\": {\"dtype\": \"bool\", \"broadcast\": [\"batch\", \"head\", \"row\"], \"causal\": \"folded into the bits\", "
-         "\"tables\": [\"bits u32 per (row, 64-key tile, lane half)\", \"class per (32 rows, tile)\", \"tile range per 128 rows\"], "
+         "\"mask\": {\"dtypes\": [\"bool\", \"bf16 (additive)\", \"f16 (additive)\"], \"broadcast\": [\"batch\", \"head\", \"row\"], \"causal\": \"folded into the bits\", "
+         "\"tables\": [\"bits u32 per (row, 64-key tile, lane half)\", \"class per (32 rows, tile)\", \"tile range per 128 rows\", \"bias values of class-3 tiles (float masks)\"], "
          "\"fully_masked_row\": 0}, "
          "\"lse\": {\"head_dims\": [64, 128], \"block_m\": 128, \"block_n\": 64, \"threads\": 256, \"mfma\": \"v_mfma_f32_32x32x16_{bf16,f16}\", "
          "\"causal\": \"bottom-right, q_len <= kv_len\"}}";

@@ -46,7 +46,8 @@ inline int kv_pad(int skv) { return (skv + SAGE_KV_PAD - 1) / SAGE_KV_PAD * SAGE
 // sage_mask.h, inside the two quantization launches).
 // bits: one 32-bit word per (row, 64-key tile, lane half hf): bit 16 kb + v is the visibility of the key that the QK
 // accumulator gives lane (query, hf) in register v of 32-key block kb, i.e. key 64 t + 32 kb + 8 (v / 4) + 4 hf + v % 4.
-// cls: per (32-row group, tile) 0 = no row sees a key of the tile, 1 = every row sees every key, 2 = mixed.  range:
+// cls: per (32-row group, tile) 0 = no row sees a key of the tile, 1 = every row sees every key (with a zero bias),
+// 2 = mixed visibility, 3 = an additive bias (values in `bias`, -inf where masked).  range:
 // per 128-row block, the first tile and one past the last tile of class != 0 in any of its four groups.  Strides are
 // in words / entries; 0 broadcasts (a mask without a batch, head or row axis).  The three tables are also passed to
 // the kernel as __restrict__ arguments of their own (global loads of the words, scalar loads of classes and ranges).
@@ -54,6 +55,7 @@ struct MaskTabs {
   const uint32_t* bits;
   const int* cls;
   const int2* range;
+  const uint16_t* bias;   // additive masks: 32 values per bits word (class-3 tiles), strides = the bits' x 32
   int64_t bsb, bsh, bsq;  // bits: batch, head, row strides (a tile adds 2 words)
   int64_t csb, csh, csg;  // cls: batch, head, 32-row group strides (a tile adds 1)
   int64_t rsb, rsh;       // range: batch, head strides (a 128-row block adds 1)

@@ -1,5 +1,5 @@
-// Boolean attention masks (torch SDPA's bool attn_mask, True = attend): the tables that the mask variant of
-// attn_kernel reads, and the one-call masked forward.
+// Attention masks with torch SDPA's semantics (bool: True = attend; float: added to the scaled scores, -inf =
+// masked): the tables that the mask variant of attn_kernel reads, and the one-call masked forward.
 //
 // The reference has no masked kernel: src/rdna4_sage/__init__.py:78-79 sends every call with an attn_mask to torch
 // SDPA.  Here the mask is turned, on the GPU and in the call's stream, into
@@ -7,7 +7,9 @@
 //         accumulator (bit 16 kb + v <-> key 64 t + 32 kb + 8 (v / 4) + 4 hf + v % 4), so the kernel masks a score
 //         with one bit extract and one bit select;
 //   cls   one entry per (32-row group, tile): 0 = no row sees a key of the tile (the wave skips it), 1 = every row
-//         sees every key (the mask-free tile body), 2 = mixed (the bit-masked body);
+//         sees every key with a zero bias (the mask-free tile body), 2 = mixed visibility (the bit-masked body),
+//         3 = an additive bias (float masks only: the biased body);
+//   bias  float masks: the 16-bit values of class-3 tiles in the bits' lane order, 32 per word;
 //   range one (first, last + 1) tile pair per 128-row block (an attention workgroup's rows): the tiles outside it
 //         are not visited at all.
 // Keys past kv_len and, with the causal flag, keys past the bottom-right diagonal are folded into the bits.  The
@@ -31,10 +33,13 @@ int attn_mask_impl(const int8_t* q8, const float* qs, const int8_t* k8, const fl
 struct MaskShape {
   int mb, mh, mq, mg, nt, nrb;
   int64_t bits_words, cls_entries, range_entries;
+  bool additive;  // a 16-bit float mask: the bias table is needed
 };
 
-static MaskShape mask_shape(int B, int H, int Sq, int Skv, int64_t msb, int64_t msh, int64_t msq, int causal) {
+static MaskShape mask_shape(int B, int H, int Sq, int Skv, int64_t msb, int64_t msh, int64_t msq, int causal,
+                            int mask_dtype) {
   MaskShape m;
+  m.additive = mask_dtype != SAGE_DTYPE_BOOL;
   m.mb = msb == 0 ? 1 : B;
   m.mh = msh == 0 ? 1 : H;
   const bool rows = msq != 0 || causal;
@@ -51,9 +56,9 @@ static MaskShape mask_shape(int B, int H, int Sq, int Skv, int64_t msb, int64_t 
 static int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
 // Workspace of sage_forward_masked: the attention plan's split state, the per-chunk V maxima, the bits, the classes,
-// the ranges (each 256-byte aligned).
+// the ranges, and for a float mask the bias values (each 256-byte aligned).
 struct MaskWorkspace {
-  int64_t attn, vpart, bits, cls, range, total;
+  int64_t attn, vpart, bits, cls, range, bias, total;
 };
 
 static int mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, const MaskShape& m, MaskWorkspace* w) {
@@ -63,21 +68,25 @@ static int mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, const M
   w->bits = w->vpart + align256(vamax_partial_bytes(B, Hkv, Skv, D));
   w->cls = w->bits + align256(m.bits_words * 4);
   w->range = w->cls + align256(m.cls_entries * 4);
-  w->total = w->range + align256(m.range_entries * 8);
+  w->bias = w->range + align256(m.range_entries * 8);
+  w->total = w->bias + (m.additive ? align256(m.bits_words * 32 * 2) : 0);
   return SAGE_OK;
 }
 
-static int check_mask_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t msb, int64_t msh,
-                            int64_t msq, const char* who) {
+static int check_mask_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int mask_dtype, int64_t msb,
+                            int64_t msh, int64_t msq, const char* who) {
   SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "%s: sizes must be positive", who);
   SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
   if (!head_dim_ok(D)) return fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 96, 128, 256)", who, D);
   if (causal && Sq > Skv) return fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len <= kv_len", who);
   SAGE_REQUIRE(msb >= 0 && msh >= 0 && msq >= 0, "%s: mask strides (%lld, %lld, %lld) must be non-negative", who,
                (long long)msb, (long long)msh, (long long)msq);
-  const MaskShape m = mask_shape(B, H, Sq, Skv, msb, msh, msq, causal);
-  // the kernel addresses one (batch, head) slice of the bits with a 32-bit byte offset
-  SAGE_REQUIRE((int64_t)m.mq * m.nt * 8 < (1ll << 31), "%s: mask of %d rows x %d keys too large", who, Sq, Skv);
+  if (mask_dtype != SAGE_DTYPE_BOOL && mask_dtype != SAGE_DTYPE_BF16 && mask_dtype != SAGE_DTYPE_F16)
+    return fail(SAGE_ERR_UNSUPPORTED, "%s: mask dtype code %d (bool=2, bf16=0, f16=1)", who, mask_dtype);
+  const MaskShape m = mask_shape(B, H, Sq, Skv, msb, msh, msq, causal, mask_dtype);
+  // the kernel addresses one (batch, head) slice of the bits (and of the bias values: 16x) with a 32-bit byte offset
+  SAGE_REQUIRE((int64_t)m.mq * m.nt * (m.additive ? 128 : 8) < (1ll << 31), "%s: mask of %d rows x %d keys too large",
+               who, Sq, Skv);
   SAGE_REQUIRE(m.cls_entries < (1ll << 31) && (int64_t)B * H * ((Sq + 127) / 128) * 16 < (1ll << 31),
                "%s: too many query tiles", who);
   SAGE_REQUIRE((int64_t)layout_dim(D) * kv_pad(Skv) < (1ll << 31), "%s: kv_len %d too long", who, Skv);
@@ -88,14 +97,14 @@ static int check_mask_shape(int B, int H, int Hkv, int Sq, int Skv, int D, int c
 
 extern "C" {
 
-int sage_mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int64_t msb, int64_t msh,
-                        int64_t msq, int64_t* workspace_bytes) {
+int sage_mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causal, int mask_dtype, int64_t msb,
+                        int64_t msh, int64_t msq, int64_t* workspace_bytes) {
   sage::clear_error();
   const char* who = "sage_mask_workspace";
   SAGE_REQUIRE(workspace_bytes != nullptr, "%s: workspace_bytes is NULL", who);
-  int rc = sage::check_mask_shape(B, H, Hkv, Sq, Skv, D, causal, msb, msh, msq, who);
+  int rc = sage::check_mask_shape(B, H, Hkv, Sq, Skv, D, causal, mask_dtype, msb, msh, msq, who);
   if (rc) return rc;
-  const sage::MaskShape m = sage::mask_shape(B, H, Sq, Skv, msb, msh, msq, causal);
+  const sage::MaskShape m = sage::mask_shape(B, H, Sq, Skv, msb, msh, msq, causal, mask_dtype);
   sage::MaskWorkspace w;
   if ((rc = sage::mask_workspace(B, H, Hkv, Sq, Skv, D, m, &w))) return rc;
   *workspace_bytes = w.total;
@@ -105,23 +114,25 @@ int sage_mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causa
 int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                         int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out, int64_t osb,
                         int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal,
-                        float qs_mul, const void* mask, int64_t msb, int64_t msh, int64_t msq, int8_t* q8, float* qs,
-                        int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace, int64_t workspace_bytes,
-                        void* stream) {
+                        float qs_mul, const void* mask, int mask_dtype, int64_t msb, int64_t msh, int64_t msq,
+                        int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
   sage::clear_error();
   const char* who = "sage_forward_masked";
   // everything is validated before the first launch, so a bad call leaves the stream untouched
-  int rc = sage::check_mask_shape(B, H, Hkv, Sq, Skv, D, causal, msb, msh, msq, who);
+  int rc = sage::check_mask_shape(B, H, Hkv, Sq, Skv, D, causal, mask_dtype, msb, msh, msq, who);
   if (rc) return rc;
   if (dtype != SAGE_DTYPE_BF16 && dtype != SAGE_DTYPE_F16)
     return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: dtype code %d (bf16=0, f16=1)", who, dtype);
+  if (mask_dtype != SAGE_DTYPE_BOOL && mask_dtype != dtype)
+    return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: a float mask must have the inputs' dtype", who);
   SAGE_REQUIRE(mask != nullptr, "%s: mask is NULL", who);
   SAGE_REQUIRE(out != nullptr && sage::aligned16(out), "%s: out must be non-NULL and 16-byte aligned", who);
   SAGE_REQUIRE(osb % 8 == 0 && oss % 8 == 0 && osh % 8 == 0 && osb >= 0 && oss >= 0 && osh >= 0,
                "%s: out strides must be non-negative multiples of 8 elements", who);
   SAGE_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 255u) == 0,
                "%s: workspace must be non-NULL and 256-byte aligned", who);
-  const sage::MaskShape m = sage::mask_shape(B, H, Sq, Skv, msb, msh, msq, causal);
+  const sage::MaskShape m = sage::mask_shape(B, H, Sq, Skv, msb, msh, msq, causal, mask_dtype);
   sage::MaskWorkspace w;
   if ((rc = sage::mask_workspace(B, H, Hkv, Sq, Skv, D, m, &w))) return rc;
   SAGE_REQUIRE(workspace_bytes >= w.total, "%s: workspace of %lld bytes, the call needs %lld", who,
@@ -133,7 +144,8 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
   int2* range = reinterpret_cast<int2*>(ws + w.range);
   float* vpart = reinterpret_cast<float*>(ws + w.vpart);
   sage::MaskPrep mp;
-  mp.mask = static_cast<const uint8_t*>(mask);
+  mp.mask = mask;
+  mp.mdt = mask_dtype;
   mp.msb = msb;
   mp.msh = msh;
   mp.msq = msq;
@@ -145,8 +157,11 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
   mp.Sq = Sq;
   mp.Skv = Skv;
   mp.causal = causal;
-  mp.a4 = ((uintptr_t)mask & 3u) == 0 && msb % 4 == 0 && msh % 4 == 0 && msq % 4 == 0;
+  // a run of 4 keys as one load: 4 bytes (bool) or 8 bytes (16-bit) aligned rows
+  const unsigned run_bytes = mask_dtype == SAGE_DTYPE_BOOL ? 4u : 8u;
+  mp.a4 = ((uintptr_t)mask % run_bytes) == 0 && msb % 4 == 0 && msh % 4 == 0 && msq % 4 == 0;
   mp.bits = bits;
+  mp.bias = m.additive ? reinterpret_cast<uint16_t*>(ws + w.bias) : nullptr;
   mp.cls = cls;
   mp.range = range;
   mp.nrange = (int)m.range_entries;
@@ -158,6 +173,7 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
   const sage::MaskTabs mt{bits,
                           cls,
                           range,
+                          mp.bias,
                           m.mb > 1 ? (int64_t)m.mh * m.mq * m.nt * 2 : 0,
                           m.mh > 1 ? (int64_t)m.mq * m.nt * 2 : 0,
                           m.mq > 1 ? (int64_t)m.nt * 2 : 0,

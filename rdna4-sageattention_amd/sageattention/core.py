@@ -3,8 +3,9 @@
 Every public function of SageAttention 2.2 keeps its signature (reference: src/sageattention/core.py:60-142).  All of
 them run the same path (Hadamard-rotated int8 Q K^T, fp8 P V with per-channel V scales); kernel-selection arguments
 such as qk_quant_gran, pv_accum_dtype, smooth_k, smooth_v or value_dtype are accepted and ignored.  Calls the gfx950
-kernels cannot run or would not win on (float masks, small problems, unsupported head dims or GPUs) use torch SDPA, so
-the functions work on any device torch supports; boolean masks run on the kernels.
+kernels cannot run or would not win on (small problems, unsupported head dims or GPUs, masks of another dtype) use torch
+SDPA, so the functions work on any device torch supports; bool and additive masks of the inputs' dtype run on the
+kernels.
 """
 from typing import Any, Optional
 
@@ -67,8 +68,8 @@ def sageattn(
 ):
     """Attention for [B, H, L, D] ("HND") or [B, L, H, D] ("NHD") fp16 / bf16 tensors; returns the input layout and
     dtype, plus the row logsumexp [B, H, q_len] when return_lse is True.  Causal masks are bottom-right aligned.
-    There is no attn_mask parameter (ComfyUI reads the signature); a boolean mask passed as a keyword runs on the
-    kernel, a float mask goes to SDPA.  The LSE, as the reference's, ignores the mask."""
+    There is no attn_mask parameter (ComfyUI reads the signature); a mask passed as a keyword (bool, or additive of
+    the inputs' dtype) runs on the kernel.  The LSE, as the reference's, ignores the mask."""
     out = cdna4_sage.sageattn(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal, sm_scale=sm_scale,
                               attn_mask=kwargs.get("attn_mask"))
     if return_lse:

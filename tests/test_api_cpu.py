@@ -178,25 +178,34 @@ def test_varlen_matches_per_sequence_attention():
 
 
 def test_mask_view_strides_and_rejections():
-    """The boolean mask as the kernel reads it: broadcast axes at stride 0, the key axis contiguous (materialised
-    alone when it is not), byte strides of (batch, head, row); float and non-broadcastable masks are rejected."""
+    """The mask as the kernel reads it: broadcast axes at stride 0, the key axis contiguous (materialised alone when
+    it is not), element strides of (batch, head, row), the dtype code (bool, or an additive mask of q's dtype);
+    masks of another dtype and non-broadcastable masks are rejected."""
+    from cdna4_sage import _capi
     from cdna4_sage._attention import Unsupported, mask_view
-    q = torch.zeros(2, 4, 6, 64)        # HND: B=2, H=4, Sq=6
-    k = torch.zeros(2, 2, 10, 64)       # Skv=10
+    q = torch.zeros(2, 4, 6, 64, dtype=torch.bfloat16)   # HND: B=2, H=4, Sq=6
+    k = torch.zeros(2, 2, 10, 64, dtype=torch.bfloat16)  # Skv=10
     pad = torch.ones(2, 1, 1, 10, dtype=torch.bool)
-    m, st = mask_view(pad, q, k, "HND")
+    m, code, st = mask_view(pad, q, k, "HND")
     assert m.shape == (2, 4, 6, 10) and st == (10, 0, 0) and m.data_ptr() == pad.data_ptr()
-    m, st = mask_view(torch.ones(6, 10, dtype=torch.bool), q, k, "HND")
+    assert code == _capi.DTYPE_BOOL
+    m, code, st = mask_view(torch.ones(6, 10, dtype=torch.bool), q, k, "HND")
     assert st == (0, 0, 10)
-    m, st = mask_view(torch.ones(10, dtype=torch.bool), q.transpose(1, 2), k.transpose(1, 2), "NHD")
+    m, code, st = mask_view(torch.ones(10, dtype=torch.bool), q.transpose(1, 2), k.transpose(1, 2), "NHD")
     assert st == (0, 0, 0)
     full = torch.rand(2, 4, 10, 6) > 0.5
-    m, st = mask_view(full.transpose(2, 3), q, k, "HND")       # key axis not contiguous: materialised
+    m, code, st = mask_view(full.transpose(2, 3), q, k, "HND")       # key axis not contiguous: materialised
     assert m.stride(3) == 1 and torch.equal(m, full.transpose(2, 3)) and st == (240, 60, 10)
     col = torch.rand(2, 1, 6, 1) > 0.5                           # broadcast over keys: only the key axis is filled in
-    m, st = mask_view(col, q, k, "HND")
+    m, code, st = mask_view(col, q, k, "HND")
     assert m.stride(3) == 1 and st == (60, 0, 10) and torch.equal(m, col.expand(2, 4, 6, 10))
-    for bad in (torch.zeros(6, 10), torch.ones(3, 1, 6, 10, dtype=torch.bool), torch.ones(1, 1, 1, 1, 10, dtype=torch.bool)):
+    bias = torch.randn(1, 4, 6, 10).to(torch.bfloat16)           # additive mask of q's dtype
+    m, code, st = mask_view(bias, q, k, "HND")
+    assert code == _capi.DTYPE_BF16 and st == (0, 60, 10) and m.dtype == torch.bfloat16
+    m, code, st = mask_view(torch.zeros(6, 10, dtype=torch.float16), q.half(), k.half(), "HND")
+    assert code == _capi.DTYPE_F16
+    for bad in (torch.zeros(6, 10), torch.zeros(6, 10, dtype=torch.float16), torch.ones(3, 1, 6, 10, dtype=torch.bool),
+                torch.ones(1, 1, 1, 1, 10, dtype=torch.bool)):
         with pytest.raises(Unsupported):
             mask_view(bad, q, k, "HND")
 

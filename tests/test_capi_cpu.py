@@ -159,8 +159,8 @@ def test_masked_forward_validates_before_launching():
     lib = _capi.lib()
     args = dict(q=P, qsb=0, qss=128, qsh=0, k=P, ksb=0, kss=128, ksh=0, v=P, vsb=0, vss=128, vsh=0, out=P, osb=0,
                 oss=128, osh=128, B=1, H=4, Hkv=2, Sq=80, Skv=200, D=128, dtype=0, causal=0, qs_mul=1.0,
-                mask=P, msb=0, msh=0, msq=200, q8=P, qs=P, k8=P, ks=P, v8t=P, vs=P, ws=P, ws_bytes=1 << 30,
-                stream=None)
+                mask=P, mask_dtype=_capi.DTYPE_BOOL, msb=0, msh=0, msq=200, q8=P, qs=P, k8=P, ks=P, v8t=P, vs=P, ws=P,
+                ws_bytes=1 << 30, stream=None)
 
     def call(**kw):
         a = dict(args, **kw)
@@ -177,8 +177,13 @@ def test_masked_forward_validates_before_launching():
     assert call(ws=None) == _capi.SAGE_ERR_INVALID and "workspace" in _err()
     assert call(ws=P + 16) == _capi.SAGE_ERR_INVALID and "256-byte" in _err()
     assert call(Sq=1 << 20, Skv=1 << 30) == _capi.SAGE_ERR_INVALID and "too large" in _err()
+    assert call(mask_dtype=7) == _capi.SAGE_ERR_UNSUPPORTED and "mask dtype" in _err()
+    assert call(mask_dtype=_capi.DTYPE_F16) == _capi.SAGE_ERR_UNSUPPORTED and "inputs' dtype" in _err()
+    # the bias values of an additive mask make its per-(batch, head) tables 16x larger than a bool mask's
+    assert call(mask_dtype=_capi.DTYPE_BF16, Sq=1 << 18, Skv=1 << 17) == _capi.SAGE_ERR_INVALID and "too large" in _err()
     ws = ctypes.c_int64(-1)
-    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 96, 1, 0, 0, -5, ctypes.byref(ws)) == _capi.SAGE_ERR_INVALID
-    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 80, 0, 0, 0, 0, ctypes.byref(ws)) == _capi.SAGE_ERR_UNSUPPORTED
-    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 128, 0, 0, 0, 0, None) == _capi.SAGE_ERR_INVALID
+    B = _capi.DTYPE_BOOL
+    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 96, 1, B, 0, 0, -5, ctypes.byref(ws)) == _capi.SAGE_ERR_INVALID
+    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 80, 0, B, 0, 0, 0, ctypes.byref(ws)) == _capi.SAGE_ERR_UNSUPPORTED
+    assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 128, 0, B, 0, 0, 0, None) == _capi.SAGE_ERR_INVALID
     assert ws.value == -1

@@ -1,5 +1,5 @@
-"""Boolean attn_mask on the gfx950 kernel (sage_forward_masked) vs the CPU emulation with the same mask and vs the
-float64 masked softmax.
+"""attn_mask on the gfx950 kernel (sage_forward_masked: bool masks, and additive float masks of the inputs' dtype) vs
+the CPU emulation with the same mask and vs the float64 masked softmax.
 
 Tolerances as for the unmasked kernel: max |out - emulation| <= 2e-2 (emulation at the kernel's 64-key tile and
 split plan) and cosine >= 0.999 against float attention with the mask.  Identities: an all-True mask gives the
@@ -36,7 +36,7 @@ def _emulate(q, k, v, layout, causal, mask, split, out_dtype):
     qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
     q8, qs = orc.quant_q(qn)
     k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(kn.shape[2]))
-    m = mask.cpu().numpy()
+    m = mask.cpu().numpy() if mask.dtype == torch.bool else mask.float().cpu().numpy()
     emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=64, out_dtype=out_dtype,
                         kv_split=split, attn_mask=m)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, attn_mask=m)
@@ -164,10 +164,67 @@ def test_sageattn_routes_bool_masks_to_the_kernel(dev, monkeypatch):
     assert cosine(kern.float().cpu().numpy(), ref.cpu().numpy()) >= COS
     fmask = torch.zeros(1, 1, 1, 1024, device=dev, dtype=torch.bfloat16)
     fmask[..., 900:] = float("-inf")
-    sd = cdna4_sage._torch_sdpa(q, k, v, attn_mask=fmask)
-    assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=fmask), sd)
+    assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=fmask), kern)   # the same mask as an additive one
     monkeypatch.setattr(cdna4_sage, "NATIVE_MASK", False)
     assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=mask), cdna4_sage._torch_sdpa(q, k, v, attn_mask=mask))
+
+
+def _alibi(H, Sq, Skv, slope=0.03):
+    rel = (torch.arange(Sq)[:, None] + (Skv - Sq) - torch.arange(Skv)[None, :]).abs().float()
+    return -(slope * torch.arange(1, H + 1).float())[:, None, None] * rel[None]    # [H, Sq, Skv]
+
+
+FLOAT_CASES = [
+    # name, (B, H, Hkv, Sq, Skv, D, dtype, layout, causal), mask builder (float32, cast to the inputs' dtype)
+    ("alibi", (1, 2, 2, 300, 700, 128, torch.bfloat16, "HND", False), lambda: _alibi(2, 300, 700)[None]),
+    ("alibi causal fp16", (1, 2, 2, 257, 600, 128, torch.float16, "NHD", True), lambda: _alibi(2, 257, 600)[None]),
+    ("padding as -inf + bias tiles", (2, 2, 1, 200, 1031, 64, torch.bfloat16, "HND", False), None),
+    ("per-row bias, GQA d256", (1, 4, 2, 130, 333, 256, torch.bfloat16, "HND", False),
+     lambda: torch.randn(1, 4, 130, 1) * 2.0),
+]
+
+
+@pytest.mark.parametrize("name,shape,make_mask", FLOAT_CASES, ids=[c[0] for c in FLOAT_CASES])
+def test_float_mask_vs_emulation(dev, name, shape, make_mask):
+    B, H, Hkv, Sq, Skv, D, dt, layout, causal = shape
+    q, k, v = _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=Sq + Skv + 7)
+    if make_mask is None:
+        # zero tiles, -inf tiles (padding past 900 keys in batch 1), and tiles with a general bias (keys 128-255)
+        mask = torch.zeros(B, 1, Sq, Skv)
+        mask[1, :, :, 900:] = float("-inf")
+        mask[:, :, :, 128:256] = torch.linspace(-3.0, 2.0, 128)
+    else:
+        mask = make_mask()
+    mask = mask.to(dt)
+    print(f"case {name}: B={B} H={H} Hkv={Hkv} Sq={Sq} Skv={Skv} D={D} {dt} {layout} causal={causal} "
+          f"mask {tuple(mask.shape)}", flush=True)
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), tensor_layout=layout, is_causal=causal,
+                               attn_mask=mask.to(dev))
+    got = hnd_np(out, layout)
+    assert np.isfinite(got).all()
+    split = kv_split(dev, B, H, Sq, Skv, D, False)
+    full = torch.broadcast_to(mask, (B, H, Sq, Skv))
+    emu, ref = _emulate(q, k, v, layout, causal, full, split, "bf16" if dt == torch.bfloat16 else "f16")
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS, err
+    assert cosine(got, ref) >= COS
+
+
+def test_float_mask_identities(dev):
+    """An all-zero float mask is the unmasked kernel bit for bit (every tile mask-free); a float mask of 0 / -inf is
+    the bool mask bit for bit (the same bit path); a bias constant along each row gives the unmasked output up to the
+    rounding of the bias path (softmax is shift-invariant)."""
+    q, k, v = (t.to(dev) for t in _inputs(1, 4, 2, 700, 1100, 128, torch.bfloat16, "HND", seed=11))
+    base = cdna4_sage.attention(q, k, v)
+    assert torch.equal(cdna4_sage.attention(q, k, v, attn_mask=torch.zeros(1100, dtype=torch.bfloat16, device=dev)),
+                       base)
+    boolm = _random((1, 4, 700, 1100), 0.7, 12).to(dev)
+    fm = torch.zeros(boolm.shape, dtype=torch.bfloat16, device=dev).masked_fill(~boolm, float("-inf"))
+    assert torch.equal(cdna4_sage.attention(q, k, v, attn_mask=fm), cdna4_sage.attention(q, k, v, attn_mask=boolm))
+    shift = (torch.randn(1, 4, 700, 1, device=dev) * 5).to(torch.bfloat16)
+    out = cdna4_sage.attention(q, k, v, attn_mask=shift)
+    assert float((out.float() - base.float()).abs().max()) <= MAX_ABS
+    assert cosine(out.float().cpu().numpy(), base.float().cpu().numpy()) >= 0.9999
 
 
 def test_masked_op_and_graph_capture(dev):

@@ -441,6 +441,47 @@ def test_masked_emulation_vs_float64_and_split():
             assert np.abs(sp[0, 1, 9] - out[0, 1, 9]).max() <= 2.0 ** -10 * np.abs(out[0, 1, 9]).max() + 1e-6
 
 
+def test_float_mask_identities_and_bias_path():
+    """Additive (float) masks.  All zero: no mask, bit for bit (every tile takes the boolean path).  Values 0 / -inf:
+    the boolean mask, bit for bit.  A constant per row (softmax is shift-invariant): the unmasked result up to the
+    rounding of the bias path, which a wrong log2(e) factor, a bias left out of the row max or a wrong rescale of m
+    would break.  An ALiBi-style bias: float64 attention with the same bias.  Split ranges merge the bias path."""
+    rng = np.random.default_rng(70)
+    q, k, v = _bf16((1, 2, 70, 64), 71), _bf16((1, 2, 200, 64), 72), _bf16((1, 2, 200, 64), 73)
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    att = lambda **kw: orc.attention(q8, qs, k8, ks, v8, vs, 200, block_n=64, out_dtype="f32", **kw)  # noqa: E731
+    base = att()
+    assert np.array_equal(att(attn_mask=np.zeros((70, 200), np.float32)), base)
+    boolm = rng.random((1, 2, 70, 200)) > 0.4
+    fm = np.where(boolm, np.float32(0), np.float32(-np.inf))
+    assert np.array_equal(att(attn_mask=fm), att(attn_mask=boolm))
+    for c in (3.0, -7.5, 40.0):
+        shifted = att(attn_mask=np.full((1, 2, 70, 1), c, np.float32) * np.ones((1, 1, 1, 200), np.float32))
+        assert np.abs(shifted - base).max() <= 1e-2 and _cos(shifted, base) >= 0.9999, c
+    wrong = att(attn_mask=np.tile(np.arange(200, dtype=np.float32) * 0.01, (70, 1)))
+    assert not np.array_equal(wrong, base)
+    slope = np.float32(0.05)
+    alibi = (-slope * np.abs(np.arange(70)[:, None] + 130 - np.arange(200)[None, :])).astype(np.float32)
+    alibi = orc.round_to_bf16(alibi)
+    for causal in (False, True):
+        out = att(attn_mask=alibi, causal=causal)
+        ref = orc.sdpa_reference(q, k, v, causal=causal, attn_mask=alibi)
+        assert _cos(out, ref) >= 0.999, causal
+        # the bias changes the result: the unbiased call is further from the biased reference
+        assert _cos(att(causal=causal), ref) < _cos(out, ref)
+    mixed = alibi.copy()
+    mixed[5] = -np.inf                         # a row that sees nothing
+    mixed[9, :150] = -np.inf                   # a row that sees only the last 50 keys
+    out = att(attn_mask=mixed)
+    assert np.isfinite(out).all() and (out[:, :, 5] == 0).all()
+    ref = orc.sdpa_reference(q, k, v, attn_mask=mixed)
+    assert _cos(out, ref) >= 0.999
+    rows = np.ones((1, 2, 70), dtype=bool)
+    sp = att(attn_mask=mixed, kv_split=(3, rows))
+    assert np.isfinite(sp).all() and (sp[:, :, 5] == 0).all() and _cos(sp, ref) >= _cos(out, ref) - 1e-4
+
+
 def test_split_rows_numbering():
     r = orc.split_rows(2, 3, 300, n_full=7)          # q_tiles = 3: tile = (b * 3 + h) * 3 + row // 128
     assert r.shape == (2, 3, 300)
