@@ -1,7 +1,7 @@
-// Boolean attention masks: the device work that turns a torch bool mask into the tables the attention kernel's mask
-// variant reads (MaskTabs in sage_host.h).  It runs as extra workgroups of sage_forward's two quantization launches
-// (no launch of its own): the bits and classes in the first, the per-workgroup tile ranges in the second, which
-// stream order places after the first.
+// Attention masks (bool, or additive bf16 / fp16): the device work that turns a torch mask into the tables the
+// attention kernel's mask variant reads (MaskTabs in sage_host.h).  It runs as extra workgroups of sage_forward's
+// two quantization launches (no launch of its own): the bits, classes and bias values in the first, the
+// per-workgroup tile ranges in the second, which stream order places after the first.
 #pragma once
 
 #include "sage_common.h"
