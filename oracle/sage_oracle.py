@@ -29,9 +29,9 @@ What each function restates (paths relative to the reference checkout):
                         accumulation, epilogue (O * ((1/448) / l)) * VS.  ``block_n`` is the KV tile of the
                         online softmax: 32 in the reference (kernel_build/compile_attn.py:109), 64 in this
                         build's gfx950 kernel.  The exponent argument is the gfx950 kernel's
-                        fma(1.5 * 2^23 + S, ct, nk) form, which differs from the reference's S * ct - cl * m by
-                        the rounding of nk (at most 1.5 * ct: S moved by less than 2 units, far below the int8
-                        quantization error of S and the E4M3 step of p).
+                        fma(c + S * 2^-26, ct * 2^26, nk) form (c = fp32(1 / (2 pi))), which differs from the
+                        reference's S * ct - cl * m by the rounding of nk (at most 1.5 * ct: S moved by less than
+                        2 units, far below the int8 quantization error of S and the E4M3 step of p).
                         Bottom-right causal for any q_len / kv_len: query i sees keys j <= i + kv_len - q_len; a
                         query that sees no key (q_len > kv_len) gives a 0 row (the gfx950 convention; the reference
                         sends such calls to SDPA, so this case has no reference value).
@@ -63,7 +63,10 @@ KV_BLOCK = 32          # one K scale per 32 keys (kernel_build/build_kernels.py:
 E4M3_MAX = 448.0
 RESCALE_THRESHOLD = 8.0  # make_sage.py:219-225: keep a stale max until it is exceeded by 2^8
 LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
-SEED = 12582912.0      # 1.5 * 2^23: fp32 whose integer-valued neighbours hold int32 QK sums exactly
+# fp32(1 / (2 pi)) = 0x3E22F983, the gfx950 kernel's seed of the QK accumulators: c + S * 2^-26 is exact for
+# |S| < 2^21 (the binade [1/8, 1/4) has ulp 2^-26), so the int32 sum read as fp32 needs no conversion
+SEED = float(np.array([0x3E22F983], dtype=np.uint32).view(np.float32)[0])
+SEED_ULP = 2.0 ** -26
 
 
 # ----------------------------------------------------------------------------------------------------------
@@ -323,7 +326,8 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
     None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).
 
     Bias path (float masks, tiles of a 32-row group holding a value other than 0 and -inf), in log2 units:
-    t = fma(F, ct, fma(b, log2e, -fp32(1.5 * 2^23 * ct))) per score, the tile's row max of t against m * cl for the
+    t = fma(F, ct', fma(b, log2e, -fp32(c * ct'))) per score (F = c + S * 2^-26, ct' = ct * 2^26, c the seed), the
+    tile's row max of t against m * cl for the
     lazy rescale (m_new = m_cand * fp32(1 / cl) when it moves), p = exp2(t - cl * m_ref)."""
     B, H, Sq, D = q8.shape
     Hkv, Sp = k8.shape[1], k8.shape[2]
@@ -387,12 +391,14 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
             corr = np.exp2(((m - m_ref).astype(F32) * cl).astype(F32)).astype(F32)
         neg = (F32(0.0) - (cl * m_ref).astype(F32)).astype(F32)
         ct = (cl[..., None] * kst[:, :, None, :]).astype(F32)    # [B, H, Sq, nsub]
-        # the gfx950 kernel reads S as F = 1.5 * 2^23 + S (exact, |S| < 2^21) and folds the offset into the
-        # additive term: arg = fma(F, ct, nk), nk = neg - fp32(1.5 * 2^23 * ct).  F * ct + nk is exact in float64
-        # (both terms have the magnitude of 1.5 * 2^23 * ct and at most 48 significant bits), so rounding it once
-        # to float32 is the kernel's fma.  It equals S * ct + neg up to the two roundings of nk (<= 1.5 ct).
+        # the gfx950 kernel reads S as F = c + S * 2^-26 (exact, |S| < 2^21, c the seed) and folds the offset into
+        # the additive term: arg = fma(F, ct', nk), ct' = ct * 2^26 (exact), nk = neg - fp32(c * ct').  F * ct' + nk
+        # is exact in float64 (both terms have the magnitude of c * ct' and at most 48 significant bits), so
+        # rounding it once to float32 is the kernel's fma.  It equals S * ct + neg up to the two roundings of nk
+        # (each at most half an ulp of ~c * 2^26 * ct: <= 1.5 ct together).
+        ct = (ct * F32(2.0 ** 26)).astype(F32)
         nk = (neg[..., None] - (F32(SEED) * ct).astype(F32)).astype(F32)
-        fs = (sb + F32(SEED)).astype(F32)
+        fs = (sb * F32(SEED_ULP) + F32(SEED)).astype(F32)
         arg = (fs.astype(np.float64) * ct[..., None].astype(np.float64) + nk[..., None].astype(np.float64)).astype(F32)
         p = np.exp2(arg).astype(F32).reshape(B, H, Sq, block_n)
         if bias_rows is not None and bias_rows.any():
@@ -408,12 +414,13 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
 
 def _bias_tile(fs, ct, bt, m, cl, threshold, rows, p, corr, need, m_new):
     """The bias path of one tile for the rows in `rows` (other rows keep p, corr, need, m_new as given).  fs: the
-    seeded scores [B, H, Sq, nsub, 32]; ct [B, H, Sq, nsub]; bt: the additive mask of the tile [B, H, Sq, block_n]."""
+    seeded scores [B, H, Sq, nsub, 32]; ct [B, H, Sq, nsub] (scaled by 2^26 like the kernel's); bt: the additive
+    mask of the tile [B, H, Sq, block_n]."""
     B, H, Sq = m.shape
     nsub = ct.shape[-1]
     f64 = np.float64
     bb = bt.reshape(B, H, Sq, nsub, KV_BLOCK)
-    nseed = -(F32(SEED) * ct).astype(F32)                                 # -fp32(1.5 * 2^23 * ct)
+    nseed = -(F32(SEED) * ct).astype(F32)                                 # -fp32(c * ct')
     with np.errstate(invalid="ignore", over="ignore"):
         inner = (bb.astype(f64) * f64(F32(LOG2E)) + nseed[..., None].astype(f64)).astype(F32)
         t = (fs.astype(f64) * ct[..., None].astype(f64) + inner.astype(f64)).astype(F32)

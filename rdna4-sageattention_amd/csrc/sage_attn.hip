@@ -5,10 +5,13 @@
 //   S_ij   = sum_d Q8_id K8_jd                            (int32, exact; |S| < 2^21)
 //   rowmax = max over the tile's 32-key blocks of (max_j S_ij) * KS_block
 //   lazy rescale: m_cand = max(m, rowmax); need = (m_cand - m) * cl > 8; m_new = need ? m_cand : m
-//   p_ij   = exp2(fma(F_ij, ct, nk)) with F_ij = 1.5 * 2^23 + S_ij, ct = cl * KS_block,
-//            nk = -(cl * m_new) - fp32(1.5 * 2^23 * ct)       (<= 2^8, fits E4M3)
-//            The QK accumulators start at the bit pattern of 1.5 * 2^23, so the int32 result read as fp32 is F
-//            exactly and needs no conversion; F * ct + nk equals S * ct - cl * m_new up to the rounding of nk.
+//   p_ij   = exp2(fma(F_ij, ct, nk)) with F_ij = c + S_ij * 2^-26, ct = cl * KS_block * 2^26,
+//            nk = -(cl * m_new) - fp32(c * ct)       (<= 2^8, fits E4M3), c = fp32(1 / (2 pi)) = 0x3E22F983
+//            The QK accumulators start at the bit pattern of c, an inline constant of the MFMA (no registers
+//            hold the seed): since |S| < 2^21 the int32 result stays inside c's binade [1/8, 1/4), whose ulp is
+//            2^-26, so read as fp32 it is F exactly and needs no conversion; F * ct + nk equals
+//            S * ct - cl * m_new up to the rounding of nk.  The kernel keeps cl scaled by 2^26 and m by 2^-26
+//            (powers of two: every product and difference of the math above is the same bits, scaled).
 //   l      = corr * l + sum_j p_ij (fp32 p);  O = need ? O * corr : O;  O += e4m3(p) V8
 //   out    = (O * ((1/448) / l)) * VS
 //
@@ -69,6 +72,16 @@ template <int DT> __device__ __forceinline__ float mask_half_to_f32(uint32_t h) 
     return __uint_as_float(h << 16);
   else
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// First QK MFMA of a key block: C = the bits of fp32(1 / (2 pi)) as the instruction's inline constant.  The
+// compiler folds a splat of it into the MFMA only where the splat has a single use; the second block's MFMA would
+// make it a 16-register value live through the whole tile loop, so that one is written out.  Its result is read
+// only as the exactly overlapping C operand of the block's next MFMA, which needs no wait states.
+__device__ __forceinline__ v16i mfma_i8_seeded(v4i a, v4i b) {
+  v16i d;
+  asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494" : "=&v"(d) : "v"(a), "v"(b));
+  return d;
 }
 
 constexpr int ATT_MAX_CHUNKS = 16;
@@ -174,8 +187,9 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
 #pragma unroll
     for (int i = 0; i < NQK; ++i) qa[i] = *reinterpret_cast<const v4i*>(qp + 32 * i);
   }
-  const float cl = c0 * qs[qrow0 + qr];
-  const float rcl = 1.0f / cl;  // the bias tiles keep m in S * ks units
+  // cl of the math scaled by 2^26, m in units of S * ks * 2^-26 (the seeded accumulators below hold S * 2^-26)
+  const float cl = (c0 * qs[qrow0 + qr]) * 67108864.0f;
+  const float rcl = 1.0f / cl;  // the bias tiles keep m in S * ks * 2^-26 units
 
   // ---- KV range ----
   int kv_end = Skv;
@@ -278,7 +292,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       const v4i k0_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_]);                                         \
       const v4i k1_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_] + 32 * D);                                \
       s_[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0_, qa[i_], i_ == 0 ? seed16 : s_[0], 0, 0, 0);       \
-      s_[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], i_ == 0 ? seed16 : s_[1], 0, 0, 0);       \
+      s_[1] = i_ == 0 ? mfma_i8_seeded(k1_, qa[i_])                                                        \
+                      : __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], s_[1], 0, 0, 0);                \
     }                                                                                                      \
     float sf_[2][16];                                                                                      \
     _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
@@ -305,8 +320,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     bool need_;                                                                                            \
     float mnew_, corr_, psum_ = 0.0f;                                                                      \
     if ((MODE) == 3) {                                                                                     \
-      /* t = fma(F, ct, fma(b, log2e, -fp32(1.5 * 2^23 * ct))): the biased logit in log2 units (b = -inf for   \
-         a masked key gives -inf); the lazy rescale compares its row max with m * cl and keeps m in S * ks     \
+      /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))): the biased logit in log2 units (b = -inf for a masked \
+         key gives -inf); the lazy rescale compares its row max with m * cl and keeps m in S * ks * 2^-26      \
          units (m_new = m_cand * (1 / cl)) */                                                               \
       const float ns0_ = -(SEED_F * ct0_), ns1_ = -(SEED_F * ct1_);                                        \
       float tm_ = -INFINITY;                                                                               \
@@ -385,11 +400,12 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   int t_mask = Skv / BN;
   if (CAUSAL) t_mask = min(t_mask, max(0, (q0 + off + 1) / BN));
   t_mask = min(t_mask, t_hi);
-  // QK accumulators start at the bits of 1.5 * 2^23 (0x4B400000): the int32 sum read as fp32 is 1.5 * 2^23 + S
-  constexpr float SEED_F = 12582912.0f;
+  // QK accumulators start at the bits of c = fp32(1 / (2 pi)) (0x3E22F983, which the compiler encodes as the
+  // MFMA's inline constant): the int32 sum read as fp32 is c + S * 2^-26, exactly
+  constexpr float SEED_F = 0.15915494f;
   v16i seed16;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) seed16[v] = 0x4B400000;
+  for (int v = 0; v < 16; ++v) seed16[v] = 0x3E22F983;
   if (t_lo < t_hi) SAGE_ISSUE_TILE(t_lo, t_lo & 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -486,7 +502,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     const int64_t units = (int64_t)(total - n_full) * chunks;
     if (hf == 0)
       reinterpret_cast<float2*>(reinterpret_cast<uint8_t*>(part) + ws_ml_offset(units, D))[(int64_t)unit * ATT_BM + q] =
-          make_float2(m, lt);
+          make_float2(m * 67108864.0f, lt);  // m in S * ks units, as the merge kernel's cl expects
     return;
   }
   const float inv = lt > 0.0f ? (1.0f / 448.0f) / lt : 0.0f;  // a row without any visible key is written as 0

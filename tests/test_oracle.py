@@ -238,8 +238,9 @@ def test_emulation_vs_float64_attention(block_n, causal):
 
 
 def test_emulation_single_key_returns_dequantized_v():
-    """One key: p = exp2(arg) with arg = 0 up to the two roundings of nk = neg - fp32(1.5 * 2^23 * ct), each at most
-    half an ulp of ~1.5 * 2^23 * ct <= 0.75 * ct.  So out = dequantized V / p with |p - 1| <= 2^(1.5 ct) - 1 (the
+    """One key: p = exp2(arg) with arg = 0 up to the two roundings of nk = neg - fp32(c * 2^26 * ct) (c = 1 / (2 pi),
+    the kernel's seed), each at most half an ulp of ~c * 2^26 * ct <= 0.75 * ct.  So out = dequantized V / p with
+    |p - 1| <= 2^(1.5 ct) - 1 (the
     E4M3 cast of p is exactly 1), and nothing else may perturb it."""
     q, k, v = _bf16((1, 2, 5, 128), 12), _bf16((1, 2, 1, 128), 13), _bf16((1, 2, 1, 128), 14)
     q8, qs = orc.quant_q(q)
@@ -333,8 +334,9 @@ def test_emulation_softmax_bookkeeping_gives_exact_lse():
         logit2 = s * cl[..., None].astype(np.float64) * ksr[:, :, None, :]
         mx = logit2.max(-1)
         exact = mx + np.log2(np.exp2(logit2 - mx[..., None]).sum(-1))
-        # every exponent argument is within 1.5 ct + 2^-24 |cl m| of S ct - cl m: nk = neg - fp32(1.5 * 2^23 * ct)
-        # rounds twice, each time by at most half an ulp of ~1.5 * 2^23 * ct; the logsumexp moves by at most that
+        # every exponent argument is within 1.5 ct + 2^-24 |cl m| of S ct - cl m: nk = neg - fp32(c * 2^26 * ct)
+        # rounds twice, each time by at most half an ulp of ~c * 2^26 * ct <= 0.75 ct; the logsumexp moves by at
+        # most that
         ct_max = (cl[..., None].astype(np.float64) * ks[:, :, None, :]).max(-1)
         bound = 1.51 * ct_max + 2.0 ** -23 * np.abs(cl * m) + 2e-5
         assert (np.abs(lse2 - exact) <= bound).all(), bn
