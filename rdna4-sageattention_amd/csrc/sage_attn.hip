@@ -318,7 +318,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
     bool need_;                                                                                            \
-    float mnew_, corr_, psum_ = 0.0f;                                                                      \
+    float mnew_, carg_, psum_ = 0.0f;                                                                      \
     if ((MODE) == 3) {                                                                                     \
       /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))): the biased logit in log2 units (b = -inf for a masked \
          key gives -inf); the lazy rescale compares its row max with m * cl and keeps m in S * ks * 2^-26      \
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       need_ = (mcand_ - mc_) > 8.0f;                                                                       \
       mnew_ = need_ ? mcand_ * rcl : m;                                                                    \
       const float mref_ = mnew_ == -INFINITY ? 0.0f : mnew_;                                               \
-      corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                                    \
+      carg_ = (m - mref_) * cl;                                                                            \
       const float negl_ = 0.0f - cl * mref_;                                                               \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           psum_ += sf_[kb_][v_];                                                                           \
         }                                                                                                  \
     } else {                                                                                               \
-      /* block maxima on the bit patterns: the scores are positive floats (1.5 * 2^23 + S) or -inf, whose     \
+      /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose      \
          int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */          \
       int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                             \
       _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                  \
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets  \
          from 0 instead of -inf keep corr and the exponents free of NaN */                                 \
       const float mref_ = ((MODE) != 0 && mnew_ == -INFINITY) ? 0.0f : mnew_;                             \
-      corr_ = __builtin_amdgcn_exp2f((m - mref_) * cl);                                                    \
+      carg_ = (m - mref_) * cl;                                                                            \
       const float neg_ = 0.0f - cl * mref_;                                                                \
       const float nk0_ = neg_ - SEED_F * ct0_, nk1_ = neg_ - SEED_F * ct1_;                                \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
@@ -375,12 +375,16 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
         psum_ += sf_[1][v_];                                                                               \
       }                                                                                                    \
     }                                                                                                      \
-    l = corr_ * l + psum_;                                                                                 \
-    m = mnew_;                                                                                             \
+    /* corr = exp2(carg): 1 in a lane whose max did not move (carg = 0), so the exponential is taken only in   \
+       the rare tiles in which some lane of the wave rescales */                                            \
+    float corr_ = 1.0f;                                                                                    \
     if (__ballot(need_) != 0) {                                                                            \
+      corr_ = __builtin_amdgcn_exp2f(carg_);                                                               \
       _Pragma("unroll") for (int i_ = 0; i_ < NPV; ++i_)                                                   \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) o[i_][v_] *= corr_;                              \
     }                                                                                                      \
+    l = corr_ * l + psum_;                                                                                 \
+    m = mnew_;                                                                                             \
     _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                     \
       const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                         \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
