@@ -2,6 +2,11 @@
 
 Tolerances (north star): max |out - emulation| <= 2e-2 with the emulation run at the kernel's own 64-key tile, and
 cosine >= 0.999 against float attention; the reference's own gate is cosine > 0.998 (tests/test_attention.py:175).
+Beyond the north star, the kernel follows the emulation element by element: the exp2 implementation and the fp32
+summation order inside the PV MFMA are the only differences, so most output elements are the emulation's bits and the
+rest move by a probability whose E4M3 rounding flipped.  Measured on these cases: 98.5-99% (bf16) and 91-95% (fp16)
+of the elements bit-identical, the largest difference 0.4% of the largest |output|; the test asserts >= 95% / 85%
+and 1%.
 """
 import numpy as np
 import pytest
@@ -17,6 +22,8 @@ pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
 COS = 0.999
+SAME_BITS = {torch.bfloat16: 0.95, torch.float16: 0.85}  # fraction of output elements equal to the emulation's
+MAX_REL = 1e-2                                           # max |out - emulation| / max |emulation|
 
 CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 2, 2, 300, 300, 128, torch.bfloat16, "HND", False),
@@ -70,6 +77,9 @@ def test_attention_vs_emulation(dev, B, H, Hkv, Sq, Skv, D, dt, layout, causal):
     c = cosine(got, ref)
     assert err <= MAX_ABS, err
     assert c >= COS, c
+    same = float((got == emu).mean())
+    assert same >= SAME_BITS[dt], same
+    assert err <= MAX_REL * float(np.abs(emu).max()), (err, float(np.abs(emu).max()))
 
 
 def test_sm_scale(dev):
@@ -98,7 +108,10 @@ def test_flux_config2_full(dev):
     split = kv_split(dev, cfg.B, cfg.H, cfg.S, cfg.S, cfg.D, False, heads=[21, 22])
     emu, _ = _emulate(qs_, ks_, vs_, "HND", False, split=split)
     got = out[:, 21:23].float().cpu().numpy()
-    assert float(np.abs(got - emu).max()) <= MAX_ABS
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS, err
+    assert float((got == emu).mean()) >= SAME_BITS[torch.bfloat16]
+    assert err <= MAX_REL * float(np.abs(emu).max())
 
 
 @pytest.mark.parametrize("B,H,Sq,Skv,D", [(1, 2, 600, 600, 128), (2, 4, 515, 515, 64), (3, 2, 77, 1031, 128)])
