@@ -21,6 +21,7 @@ from torch.nn.attention.bias import causal_lower_right
 from . import ops
 from ._attention import (ARCHS, HEAD_DIMS, Unsupported, attention_varlen, check_supported, device_arch, lse,
                          mask_view)
+from ._attention import attention as _attention_impl
 
 __all__ = ["sageattn", "attention", "attention_varlen", "lse", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
 __version__ = "0.1.0"
@@ -59,10 +60,14 @@ def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False, attn
     Causal attention is bottom-right aligned and needs q_len <= kv_len.  attn_mask: None, a boolean mask (True =
     attend) or an additive mask of q's dtype, broadcastable to [B, H, q_len, kv_len] as torch SDPA takes it; a query
     row that sees no key is 0."""
-    if attn_mask is None:
-        out = ops.attention(q, k, v, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
-    else:
-        out = ops.attention_masked(q, k, v, attn_mask, tensor_layout, float(sm_scale or 0.0), bool(is_causal))
+    sm = float(sm_scale or 0.0)
+    if torch.compiler.is_compiling():  # traced: the registered op, which Dynamo sees through its fake impl
+        if attn_mask is None:
+            out = ops.attention(q, k, v, tensor_layout, sm, bool(is_causal))
+        else:
+            out = ops.attention_masked(q, k, v, attn_mask, tensor_layout, sm, bool(is_causal))
+    else:  # eager: the op's implementation itself, without the dispatcher's ~20 us per call
+        out = _attention_impl(q, k, v, tensor_layout, sm if sm > 0 else None, bool(is_causal), attn_mask=attn_mask)
     return out.transpose(1, 2) if tensor_layout == "HND" else out
 
 

@@ -6,6 +6,7 @@ current stream.  Intermediates are torch-owned (caching allocator), as in the re
 """
 from __future__ import annotations
 
+import functools
 import json
 import math
 from pathlib import Path
@@ -143,35 +144,53 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False, attn_mask=N
     q, sq_ = _bsh(q, layout)
     k, sk_ = _bsh(k, layout)
     v, sv_ = _bsh(v, layout)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    di = dev.index if dev.index is not None else torch.cuda.current_device()
+    causal = bool(is_causal)
+    offs, total, ws_bytes, _, _ = _forward_layout(di, B, H, Hkv, Sq, Skv, D, causal,
+                                                  None if attn_mask is None else (mcode, *mstr))
+    # Q8, QS, K8, KS, V8T, VS and the workspace in one caching-allocator block (torch-owned, freed with the call)
+    buf = torch.empty((total,), device=dev, dtype=torch.uint8)
+    base = buf.data_ptr()
+    q8, qs, k8, ks, v8t, vs, ws = (base + o for o in offs)
+    out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
+    if attn_mask is not None:
+        args = ("sage_forward_masked", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),
+                B, H, Hkv, Sq, Skv, D, dt, int(causal), qs_fold_factor(sm_scale, D), _ptr(mask), mcode, *mstr,
+                q8, qs, k8, ks, v8t, vs, ws, ws_bytes, stream)
+    else:
+        args = ("sage_forward", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),
+                B, H, Hkv, Sq, Skv, D, dt, int(causal), qs_fold_factor(sm_scale, D),
+                q8, qs, k8, ks, v8t, vs, ws, ws_bytes, stream)
+    if di == torch.cuda.current_device():
+        _capi.call(*args)
+    else:
+        with torch.cuda.device(dev):
+            _capi.call(*args)
+    return out
+
+
+_ALIGN = 256  # every intermediate and the workspace start on a 256-byte boundary (the library needs 16 / 256)
+
+
+@functools.lru_cache(maxsize=4096)
+def _forward_layout(di: int, B: int, H: int, Hkv: int, Sq: int, Skv: int, D: int, causal: bool, mask_key=None):
+    """Byte offsets of Q8, QS, K8, KS, V8T, VS and the workspace inside one device buffer, the buffer's size, the
+    workspace's size and the layout width (128 for head_dim 96): one caching-allocator request per call instead of
+    seven.  mask_key = (mask dtype code, batch / head / row strides) for sage_forward_masked's workspace."""
     skp = _capi.kv_pad(Skv)
     dl = _capi.layout_dim(D)    # head_dim 96 is stored zero-padded to 128 channels
-    stream = torch.cuda.current_stream(dev).cuda_stream
-
-    q8 = torch.empty((B, H, Sq, dl), device=dev, dtype=torch.int8)
-    qs = torch.empty((B, H, Sq), device=dev, dtype=torch.float32)
-    k8 = torch.empty((B, Hkv, skp, dl), device=dev, dtype=torch.int8)
-    ks = torch.empty((B, Hkv, skp // KV_BLOCK), device=dev, dtype=torch.float32)
-    v8t = torch.empty((B, Hkv, dl, skp), device=dev, dtype=torch.uint8)
-    vs = torch.empty((B, Hkv, dl), device=dev, dtype=torch.float32)
-    out = torch.empty((B, Sq, H, D), device=dev, dtype=q.dtype)
-    di = dev.index if dev.index is not None else torch.cuda.current_device()
-    if attn_mask is not None:
-        ws_bytes = _capi.mask_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal), mcode, *mstr)
-        ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
-        with torch.cuda.device(dev):
-            _capi.call("sage_forward_masked", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out),
-                       *_out_strides(out), B, H, Hkv, Sq, Skv, D, dt, int(bool(is_causal)),
-                       qs_fold_factor(sm_scale, D), _ptr(mask), mcode, *mstr, _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks),
-                       _ptr(v8t), _ptr(vs), _ptr(ws), ws_bytes, stream)
-        return out
-    ws_bytes = _capi.forward_workspace(di, B, H, Hkv, Sq, Skv, D, bool(is_causal))
-    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
-    with torch.cuda.device(dev):
-        _capi.call("sage_forward", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),
-                   B, H, Hkv, Sq, Skv, D, dt, int(bool(is_causal)), qs_fold_factor(sm_scale, D),
-                   _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _ptr(v8t), _ptr(vs),
-                   _ptr(ws), ws_bytes, stream)
-    return out
+    if mask_key is None:
+        ws_bytes = _capi.forward_workspace(di, B, H, Hkv, Sq, Skv, D, causal)
+    else:
+        ws_bytes = _capi.mask_workspace(di, B, H, Hkv, Sq, Skv, D, causal, *mask_key)
+    sizes = (B * H * Sq * dl, B * H * Sq * 4, B * Hkv * skp * dl, B * Hkv * (skp // KV_BLOCK) * 4,
+             B * Hkv * dl * skp, B * Hkv * dl * 4, ws_bytes)
+    offs, at = [], 0
+    for n in sizes:
+        offs.append(at)
+        at += (n + _ALIGN - 1) // _ALIGN * _ALIGN
+    return tuple(offs), max(at, _ALIGN), ws_bytes, skp, dl
 
 
 def _out_strides(out: torch.Tensor):
