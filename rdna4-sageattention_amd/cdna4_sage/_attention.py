@@ -271,19 +271,29 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q=None, max
     q, sq_ = _packed(q)
     k, sk_ = _packed(k)
     v, sv_ = _packed(v)
-    tkp, ws_bytes = _capi.varlen_layout(batch, H, Hkv, TQ, TK)
-    dl = _capi.layout_dim(D)
-    q8 = torch.empty((H, TQ, dl), device=dev, dtype=torch.int8)
-    qs = torch.empty((H, TQ), device=dev, dtype=torch.float32)
-    k8 = torch.empty((Hkv, tkp, dl), device=dev, dtype=torch.int8)
-    ks = torch.empty((Hkv, tkp // KV_BLOCK), device=dev, dtype=torch.float32)
-    v8t = torch.empty((Hkv, dl, tkp), device=dev, dtype=torch.uint8)
-    vs = torch.empty((batch, Hkv, dl), device=dev, dtype=torch.float32)
-    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+    offs, total, ws_bytes = _varlen_layout(batch, H, Hkv, TQ, TK, D)
+    # Q8 [H][TQ], QS, K8 / KS / V8T in the padded packed layout, VS [batch][Hkv] and the table workspace: one block
+    buf = torch.empty((total,), device=dev, dtype=torch.uint8)
+    q8, qs, k8, ks, v8t, vs, ws = (buf.data_ptr() + o for o in offs)
     out = torch.empty((TQ, H, D), device=dev, dtype=q.dtype)
     with torch.cuda.device(dev):
         _capi.call("sage_forward_varlen", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), out.stride(0),
                    out.stride(1), _ptr(cu_q), _ptr(cu_k), batch, H, Hkv, TQ, TK, D, DTYPES[q.dtype],
-                   int(bool(is_causal)), qs_fold_factor(sm_scale, D), _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks),
-                   _ptr(v8t), _ptr(vs), _ptr(ws), ws_bytes, torch.cuda.current_stream(dev).cuda_stream)
+                   int(bool(is_causal)), qs_fold_factor(sm_scale, D), q8, qs, k8, ks, v8t, vs, ws, ws_bytes,
+                   torch.cuda.current_stream(dev).cuda_stream)
     return out
+
+
+@functools.lru_cache(maxsize=4096)
+def _varlen_layout(batch: int, H: int, Hkv: int, TQ: int, TK: int, D: int):
+    """Byte offsets of the varlen pass's Q8, QS, K8, KS, V8T, VS and table workspace inside one device buffer, the
+    buffer's size and the workspace's size (host arithmetic of the library's sage_varlen_layout)."""
+    tkp, ws_bytes = _capi.varlen_layout(batch, H, Hkv, TQ, TK)
+    dl = _capi.layout_dim(D)
+    sizes = (H * TQ * dl, H * TQ * 4, Hkv * tkp * dl, Hkv * (tkp // KV_BLOCK) * 4, Hkv * dl * tkp,
+             batch * Hkv * dl * 4, ws_bytes)
+    offs, at = [], 0
+    for n in sizes:
+        offs.append(at)
+        at += (n + _ALIGN - 1) // _ALIGN * _ALIGN
+    return tuple(offs), max(at, _ALIGN), ws_bytes

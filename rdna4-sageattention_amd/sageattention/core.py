@@ -70,11 +70,38 @@ def sageattn(
     dtype, plus the row logsumexp [B, H, q_len] when return_lse is True.  Causal masks are bottom-right aligned.
     There is no attn_mask parameter (ComfyUI reads the signature); a mask passed as a keyword (bool, or additive of
     the inputs' dtype) runs on the kernel.  The LSE, as the reference's, ignores the mask."""
+    if (return_lse and q.is_cuda and not torch.compiler.is_compiling()
+            and not torch.cuda.is_current_stream_capturing()):
+        # the LSE pass does not depend on the attention: it runs on a side stream (default priority) concurrently with
+        # the quantizers and the attention kernel on the caller's stream, which waits for it before returning (under
+        # graph capture or tracing the two run one after the other on the caller's stream)
+        cur = torch.cuda.current_stream(q.device)
+        side = _side_stream(q.device)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            lse = _lse(q, k, tensor_layout, is_causal, sm_scale)
+        q.record_stream(side)
+        k.record_stream(side)
+        out = cdna4_sage.sageattn(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal, sm_scale=sm_scale,
+                                  attn_mask=kwargs.get("attn_mask"))
+        cur.wait_stream(side)
+        lse.record_stream(cur)
+        return out, lse
     out = cdna4_sage.sageattn(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal, sm_scale=sm_scale,
                               attn_mask=kwargs.get("attn_mask"))
     if return_lse:
         return out, _lse(q, k, tensor_layout, is_causal, sm_scale)
     return out
+
+
+_side_streams = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _side_streams:
+        _side_streams[idx] = torch.cuda.Stream(device=idx)
+    return _side_streams[idx]
 
 
 def sageattn_varlen(
