@@ -70,3 +70,26 @@ def test_lse_unsupported_and_return_lse_uses_kernel(dev):
     k = torch.randn(1, 2, 2048, 128, device=dev, dtype=torch.bfloat16)
     _, lse = sageattention.sageattn(q, k, v, is_causal=True, return_lse=True)
     torch.testing.assert_close(lse, cdna4_sage.lse(q, k, "HND", None, True), atol=0, rtol=0)
+
+
+def test_return_lse_side_stream_joins_the_callers_stream(dev):
+    """sageattn(return_lse=True) computes the LSE on a side stream; work the caller queues on its own stream right
+    after the call must see the finished LSE and output (the call joins the side stream before returning), also from a
+    non-default caller stream, and the results equal the one-stream computation bit for bit."""
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(1, 8, 4096, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, 8, 4096, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, 8, 4096, 128, generator=g).to(torch.bfloat16).to(dev)
+    ref_lse = cdna4_sage.lse(q, k, "HND", None, True)
+    ref_out = sageattention.sageattn(q, k, v, is_causal=True)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            out, lse = sageattention.sageattn(q, k, v, is_causal=True, return_lse=True)
+            lse_copy = lse * 1.0          # queued on the caller's stream right after the call
+            out_copy = out.float() * 1.0
+    s.synchronize()
+    torch.testing.assert_close(lse_copy, ref_lse, atol=0, rtol=0)
+    torch.testing.assert_close(out_copy, ref_out.float(), atol=0, rtol=0)
