@@ -406,10 +406,11 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   t_mask = min(t_mask, t_hi);
   // QK accumulators start at the bits of c = fp32(1 / (2 pi)) (0x3E22F983, which the compiler encodes as the
   // MFMA's inline constant): the int32 sum read as fp32 is c + S * 2^-26, exactly
-  constexpr float SEED_F = 0.15915494f;
+  constexpr uint32_t SEED_BITS = 0x3E22F983u;
+  constexpr float SEED_F = __builtin_bit_cast(float, SEED_BITS);
   v16i seed16;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) seed16[v] = 0x3E22F983;
+  for (int v = 0; v < 16; ++v) seed16[v] = (int)SEED_BITS;
   if (t_lo < t_hi) SAGE_ISSUE_TILE(t_lo, t_lo & 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
