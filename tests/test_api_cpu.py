@@ -220,3 +220,34 @@ def test_bool_mask_routing_without_kernel_uses_sdpa():
     out = cdna4_sage.sageattn(q, k, v, attn_mask=mask)
     ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
     assert torch.allclose(out, ref, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,H,Hkv,Sq,Skv,D", [(1, 24, 24, 4608, 4608, 128), (2, 32, 8, 8192, 8192, 64),
+                                             (3, 2, 2, 77, 1031, 96), (1, 3, 1, 1, 1, 256)])
+def test_single_block_layouts(monkeypatch, B, H, Hkv, Sq, Skv, D):
+    """The dense and varlen paths carve Q8, QS, K8, KS, V8T, VS and the workspace out of one allocation: every piece
+    starts on a 256-byte boundary, none overlaps the next, and each is as large as the library's layout needs
+    (the workspace sizes come from the library's plan queries, which need a GPU; stand-ins here)."""
+    from cdna4_sage import _attention, _capi
+
+    monkeypatch.setattr(_capi, "forward_workspace", lambda *a: 12345)
+    monkeypatch.setattr(_capi, "varlen_layout", lambda batch, H_, Hkv_, TQ, TK: ((TK // 128 + batch) * 128, 777))
+    _attention._forward_layout.cache_clear()
+    _attention._varlen_layout.cache_clear()
+    skp, dl = _capi.kv_pad(Skv), _capi.layout_dim(D)
+    offs, total, ws, skp_, dl_ = _attention._forward_layout(0, B, H, Hkv, Sq, Skv, D, False)
+    assert (skp_, dl_, ws) == (skp, dl, 12345)
+    need = [B * H * Sq * dl, B * H * Sq * 4, B * Hkv * skp * dl, B * Hkv * skp // 32 * 4, B * Hkv * dl * skp,
+            B * Hkv * dl * 4, 12345]
+    ends = [o + n for o, n in zip(offs, need)]
+    assert all(o % 256 == 0 for o in offs)
+    assert all(e <= o for e, o in zip(ends, offs[1:])) and ends[-1] <= total
+    TQ, TK = B * Sq, B * Skv
+    voffs, vtotal, vws = _attention._varlen_layout(B, H, Hkv, TQ, TK, D)
+    tkp = (TK // 128 + B) * 128
+    vneed = [H * TQ * dl, H * TQ * 4, Hkv * tkp * dl, Hkv * tkp // 32 * 4, Hkv * dl * tkp, B * Hkv * dl * 4, 777]
+    vends = [o + n for o, n in zip(voffs, vneed)]
+    assert vws == 777 and all(o % 256 == 0 for o in voffs)
+    assert all(e <= o for e, o in zip(vends, voffs[1:])) and vends[-1] <= vtotal
+    _attention._forward_layout.cache_clear()
+    _attention._varlen_layout.cache_clear()
