@@ -55,13 +55,22 @@ def is_available(device=None) -> bool:
     return device_arch(dev) in ARCHS
 
 
+def _plain_eager(*ts) -> bool:
+    """True for an eager call on plain tensors: no torch.compile / export tracing, no tensor subclass (fake or
+    functional tensors) and no active dispatch mode (make_fx and the like).  Such calls may run the op's implementation
+    directly; anything else goes through the registered op."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
+        return False
+    return all(type(t) is torch.Tensor for t in ts)
+
+
 def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False, attn_mask=None):
     """Run the int8/fp8 kernel; raises Unsupported if it cannot.  Output in the input layout and dtype.
     Causal attention is bottom-right aligned and needs q_len <= kv_len.  attn_mask: None, a boolean mask (True =
     attend) or an additive mask of q's dtype, broadcastable to [B, H, q_len, kv_len] as torch SDPA takes it; a query
     row that sees no key is 0."""
     sm = float(sm_scale or 0.0)
-    if torch.compiler.is_compiling():  # traced: the registered op, which Dynamo sees through its fake impl
+    if not _plain_eager(q, k, v):  # traced: the registered op, which tracers see through its fake impl
         if attn_mask is None:
             out = ops.attention(q, k, v, tensor_layout, sm, bool(is_causal))
         else:

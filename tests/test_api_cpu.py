@@ -117,6 +117,12 @@ def test_fake_impl_shapes():
         kvn = torch.empty(2, 300, 8, 64, dtype=torch.float16)
         o = torch.ops.rdna4_sage.attention(qn, kvn, kvn, "NHD", 0.0, False)
         assert o.shape == (2, 100, 24, 64) and o.dtype == torch.float16
+        # the Python entry points route fake tensors through the registered ops (their eager shortcut is for plain
+        # tensors only), so tracers see the fake implementation
+        assert not cdna4_sage._plain_eager(q, kv, kv)
+        assert cdna4_sage.attention(q, kv, kv, "HND").shape == (2, 24, 100, 128)
+        assert rdna4_sage.attention(qn, kvn, kvn, "NHD").shape == (2, 100, 24, 64)
+    assert cdna4_sage._plain_eager(torch.empty(1), torch.empty(1))
 
 
 @pytest.mark.parametrize("layout", ["HND", "NHD"])
