@@ -19,6 +19,10 @@ from oracle import sage_oracle as orc
 pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
+# element-level agreement with the emulation, as for the unmasked kernel (tests/test_gpu_attention.py): measured
+# 98.3-99.2% (bf16) / 93-96% (fp16) of the output elements bit-identical, largest difference 0.65% of max |output|
+SAME_BITS = {torch.bfloat16: 0.95, torch.float16: 0.85}
+MAX_REL = 1e-2
 COS = 0.999
 
 
@@ -105,6 +109,8 @@ def test_masked_attention_vs_emulation(dev, name, shape, make_mask):
     err = float(np.abs(got - emu).max())
     assert err <= MAX_ABS, err
     assert cosine(got, ref) >= COS
+    assert float((got == emu).mean()) >= SAME_BITS[dt]
+    assert err <= MAX_REL * float(np.abs(emu).max())
     if name == "random full":
         assert (got[0, 1, 7] == 0).all() and (ref[0, 1, 7] == 0).all()
         assert np.abs(got[0, 0, 9] - emu[0, 0, 9]).max() <= MAX_ABS
@@ -208,6 +214,8 @@ def test_float_mask_vs_emulation(dev, name, shape, make_mask):
     err = float(np.abs(got - emu).max())
     assert err <= MAX_ABS, err
     assert cosine(got, ref) >= COS
+    assert float((got == emu).mean()) >= SAME_BITS[dt]
+    assert err <= MAX_REL * float(np.abs(emu).max())
 
 
 def test_float_mask_identities(dev):
