@@ -67,6 +67,17 @@ LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
 # |S| < 2^21 (the binade [1/8, 1/4) has ulp 2^-26), so the int32 sum read as fp32 needs no conversion
 SEED = float(np.array([0x3E22F983], dtype=np.uint32).view(np.float32)[0])
 SEED_ULP = 2.0 ** -26
+# the gfx950 kernel's key tile: split key ranges and the classes of additive masks are per 64-key tile, whatever the
+# block_n of the online softmax
+KERNEL_TILE = 64
+
+
+def seeded(d_layout: int) -> bool:
+    """Whether the gfx950 kernel reads its scores seeded (F = c + S * 2^-26) for a layout of d_layout channels:
+    c + S * 2^-26 stays in c's binade [1/8, 1/4) for -2,292,099 <= S < 6,097,183, i.e. |S| <= 127^2 * d_layout for
+    d_layout <= 128.  Head dim 256 (|S| up to 4,129,024) converts S to fp32 instead (F = S), the reference's
+    arithmetic."""
+    return 127 * 127 * d_layout < 2292099
 
 
 # ----------------------------------------------------------------------------------------------------------
@@ -263,8 +274,9 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     holding values rounded to ``out_dtype`` ("bf16", "f16" or "f32" for no rounding).
 
     ``kv_split = (chunks, rows)``, rows a bool array [B, H, Sq], emulates the gfx950 kernel's split tiles (no
-    counterpart in the reference): for those rows the key tiles run as ``chunks`` contiguous ranges (range c =
-    tiles [c * n // chunks, (c + 1) * n // chunks)), each with its own online softmax from m = -inf, stored as
+    counterpart in the reference): for those rows the keys run as ``chunks`` contiguous ranges (range c = the
+    kernel's 64-key tiles [c * n // chunks, (c + 1) * n // chunks), n = ceil(seq_kv / 64), whatever ``block_n``),
+    each with its own online softmax from m = -inf, stored as
     (m_c, l_c, fp16(O_c / l_c)) and merged with M = max m_c, W_c = exp2((m_c - M) * cl) * l_c, L = sum W_c,
     O = sum W_c * fp16(O_c / l_c) (float32, chunk order), then the usual epilogue with L.  A range in which a row
     sees no key (l_c = 0, m_c = -inf) stores 0 and weighs 0.
@@ -274,14 +286,20 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     SDPA).  Masked scores are -inf like the causal ones, ANDed with the causal mask when both are given.  A float
     array is an additive mask (SDPA: softmax(Q K^T * scale + mask), -inf = masked), emulated as the gfx950 kernel
     runs it: per 32-row group (a wave) and key tile whose values are all 0 or -inf, the boolean path above; otherwise
-    the bias path of ``_online_softmax``."""
+    the bias path of ``_online_softmax``.  The group-and-tile classes are per 32 rows and 64 keys (the kernel's tile),
+    whatever ``block_n``."""
     B, H, Sq, D = q8.shape
     Hkv = k8.shape[1]
-    assert block_n % KV_BLOCK == 0 and H % Hkv == 0
+    assert block_n % KV_BLOCK == 0 and KERNEL_TILE % block_n == 0 and H % Hkv == 0
     grp = H // Hkv
     hk = np.arange(H) // grp
     cl = (logit_scale_base(D) * qs.astype(F32)).astype(F32)      # [B, H, Sq]
     n_tiles = (seq_kv + block_n - 1) // block_n
+    # split key ranges are whole kernel tiles: range c = kernel tiles [c * n // chunks, (c + 1) * n // chunks)
+    k_tiles = (seq_kv + KERNEL_TILE - 1) // KERNEL_TILE
+    per = KERNEL_TILE // block_n
+    def krange(c, chunks):
+        return min(c * k_tiles // chunks * per, n_tiles), min((c + 1) * k_tiles // chunks * per, n_tiles)
     if attn_mask is not None:
         attn_mask = np.asarray(attn_mask)
         if attn_mask.dtype == bool:
@@ -292,7 +310,7 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     if kv_split is not None:
         chunks, rows = kv_split
         parts = [_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold,
-                                 c * n_tiles // chunks, (c + 1) * n_tiles // chunks, attn_mask)
+                                 *krange(c, chunks), attn_mask)
                  for c in range(chunks)]
         mm = parts[0][1]
         for _, mc, _ in parts[1:]:
@@ -326,9 +344,9 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
     None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).
 
     Bias path (float masks, tiles of a 32-row group holding a value other than 0 and -inf), in log2 units:
-    t = fma(F, ct', fma(b, log2e, -fp32(c * ct'))) per score (F = c + S * 2^-26, ct' = ct * 2^26, c the seed), the
-    tile's row max of t against m * cl for the
-    lazy rescale (m_new = m_cand * fp32(1 / cl) when it moves), p = exp2(t - cl * m_ref)."""
+    t = fma(F, ct', fma(b, log2e, -fp32(c * ct'))) per score (F = c + S * 2^-26, ct' = ct * 2^26, c the seed; for
+    head dim 256 F = S, ct' = ct, c = 0), the tile's row max of t against m * cl for the lazy rescale
+    (m_new = m_cand * fp32(1 / cl) when it moves), p = exp2(t - cl * m_ref)."""
     B, H, Sq, D = q8.shape
     Hkv, Sp = k8.shape[1], k8.shape[2]
     hk = np.arange(H) // (H // Hkv)
@@ -349,7 +367,7 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
         kt[:, :, : j1 - j0] = k8f[:, :, j0:j1]
         vt = np.zeros((B, Hkv, block_n, D), dtype=F32)
         vt[:, :, : j1 - j0] = v8f[:, :, j0:j1]
-        # exact int32 scores (|S| <= 127*127*128 < 2^24, so float32 matmul is exact)
+        # exact int32 scores (|S| <= 127 * 127 * 256 < 2^24, so every float32 partial sum is exact)
         s = np.matmul(q8f, np.swapaxes(kt[:, hk], -1, -2))      # [B, H, Sq, block_n]
         mask = cols[None, :] >= seq_kv
         if causal:
@@ -365,12 +383,7 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
                 bt = np.full((B, H, Sq, block_n), -np.inf, dtype=F32)
                 bt[..., :nv] = attn_mask[..., j0:j0 + nv]
                 bt = np.where(mask, F32(-np.inf), bt).astype(F32)
-                general = (bt != 0) & (bt != -np.inf)
-                ng = (Sq + 31) // 32
-                grp = np.zeros((B, H, ng), dtype=bool)
-                for g in range(ng):
-                    grp[:, :, g] = general[:, :, 32 * g:32 * g + 32].any(axis=(-1, -2))
-                bias_rows = grp[:, :, rows // 32]                          # [B, H, Sq]: this tile takes the bias path
+                bias_rows = _bias_groups(attn_mask, seq_kv, causal, causal_off, j0 // KERNEL_TILE)
                 mask = mask | (bt == -np.inf)
         s = np.where(mask, F32(-np.inf), s).astype(F32)
         kst = np.ones((B, Hkv, nsub), dtype=F32)
@@ -391,18 +404,26 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
             corr = np.exp2(((m - m_ref).astype(F32) * cl).astype(F32)).astype(F32)
         neg = (F32(0.0) - (cl * m_ref).astype(F32)).astype(F32)
         ct = (cl[..., None] * kst[:, :, None, :]).astype(F32)    # [B, H, Sq, nsub]
-        # the gfx950 kernel reads S as F = c + S * 2^-26 (exact, |S| < 2^21, c the seed) and folds the offset into
-        # the additive term: arg = fma(F, ct', nk), ct' = ct * 2^26 (exact), nk = neg - fp32(c * ct').  F * ct' + nk
-        # is exact in float64 (both terms have the magnitude of c * ct' and at most 48 significant bits), so
-        # rounding it once to float32 is the kernel's fma.  It equals S * ct + neg up to the two roundings of nk
-        # (each at most half an ulp of ~c * 2^26 * ct: <= 1.5 ct together).
-        ct = (ct * F32(2.0 ** 26)).astype(F32)
-        nk = (neg[..., None] - (F32(SEED) * ct).astype(F32)).astype(F32)
-        fs = (sb * F32(SEED_ULP) + F32(SEED)).astype(F32)
+        if seeded(D):
+            # the gfx950 kernel reads S as F = c + S * 2^-26 (exact, c the seed) and folds the offset into the
+            # additive term: arg = fma(F, ct', nk), ct' = ct * 2^26 (exact), nk = neg - fp32(c * ct').  F * ct' + nk
+            # is exact in float64 (both terms have the magnitude of c * ct' and at most 48 significant bits), so
+            # rounding it once to float32 is the kernel's fma.  It equals S * ct + neg up to the two roundings of
+            # nk (each at most half an ulp of ~c * 2^26 * ct: <= 1.5 ct together).
+            ct = (ct * F32(2.0 ** 26)).astype(F32)
+            nk = (neg[..., None] - (F32(SEED) * ct).astype(F32)).astype(F32)
+            fs = (sb * F32(SEED_ULP) + F32(SEED)).astype(F32)
+        else:
+            # head dim 256: F = fp32(S), arg = fma(S, ct, neg), the reference's exponent (make_sage_r2.py:193-200).
+            # S * ct is exact in float64; the sum is rounded twice (float64, then float32), which differs from the
+            # fma's single rounding only when the float64 result lands on a float32 rounding boundary.
+            nk = np.broadcast_to(neg[..., None], ct.shape).astype(F32)
+            fs = sb.astype(F32)
         arg = (fs.astype(np.float64) * ct[..., None].astype(np.float64) + nk[..., None].astype(np.float64)).astype(F32)
         p = np.exp2(arg).astype(F32).reshape(B, H, Sq, block_n)
         if bias_rows is not None and bias_rows.any():
-            p, corr, need, m_new = _bias_tile(fs, ct, bt, m, cl, threshold, bias_rows, p, corr, need, m_new)
+            p, corr, need, m_new = _bias_tile(fs, ct, bt, m, cl, threshold, bias_rows, p, corr, need, m_new,
+                                              SEED if seeded(D) else 0.0)
         tile_sum = p.sum(axis=-1, dtype=F32)
         l = ((corr * l).astype(F32) + tile_sum).astype(F32)
         o = np.where(need[..., None], (o * corr[..., None]).astype(F32), o)
@@ -412,15 +433,15 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
     return o, m, l
 
 
-def _bias_tile(fs, ct, bt, m, cl, threshold, rows, p, corr, need, m_new):
+def _bias_tile(fs, ct, bt, m, cl, threshold, rows, p, corr, need, m_new, seed=SEED):
     """The bias path of one tile for the rows in `rows` (other rows keep p, corr, need, m_new as given).  fs: the
-    seeded scores [B, H, Sq, nsub, 32]; ct [B, H, Sq, nsub] (scaled by 2^26 like the kernel's); bt: the additive
-    mask of the tile [B, H, Sq, block_n]."""
+    scores as the kernel reads them [B, H, Sq, nsub, 32]; ct [B, H, Sq, nsub] (scaled by 2^26 like the kernel's
+    when seeded); bt: the additive mask of the tile [B, H, Sq, block_n]; seed: c, or 0 for unseeded scores."""
     B, H, Sq = m.shape
     nsub = ct.shape[-1]
     f64 = np.float64
     bb = bt.reshape(B, H, Sq, nsub, KV_BLOCK)
-    nseed = -(F32(SEED) * ct).astype(F32)                                 # -fp32(c * ct')
+    nseed = -(F32(seed) * ct).astype(F32)                                 # -fp32(c * ct'), -0 unseeded
     with np.errstate(invalid="ignore", over="ignore"):
         inner = (bb.astype(f64) * f64(F32(LOG2E)) + nseed[..., None].astype(f64)).astype(F32)
         t = (fs.astype(f64) * ct[..., None].astype(f64) + inner.astype(f64)).astype(F32)
@@ -439,6 +460,26 @@ def _bias_tile(fs, ct, bt, m, cl, threshold, rows, p, corr, need, m_new):
     pb = np.exp2((t + negl[..., None]).astype(F32)).astype(F32)
     return (np.where(rows[..., None], pb, p), np.where(rows, cr, corr), np.where(rows, nd, need),
             np.where(rows, mn, m_new).astype(F32))
+
+
+def _bias_groups(attn_mask, seq_kv, causal, causal_off, kt):
+    """Bool [B, H, Sq]: rows whose 32-row group (a wave of the gfx950 kernel) takes the bias path in kernel tile kt
+    (keys [64 kt, 64 kt + 64)): some value of the group's rows over the tile's keys, after the padding and causal
+    masks, is neither 0 nor -inf."""
+    B, H, Sq, _ = attn_mask.shape
+    j0 = kt * KERNEL_TILE
+    nv = max(0, min(j0 + KERNEL_TILE, seq_kv) - j0)
+    bt = np.full((B, H, Sq, KERNEL_TILE), -np.inf, dtype=F32)
+    bt[..., :nv] = attn_mask[..., j0:j0 + nv]
+    if causal:
+        cols = np.arange(j0, j0 + KERNEL_TILE)
+        bt = np.where(cols[None, :] > np.arange(Sq)[:, None] + causal_off, F32(-np.inf), bt).astype(F32)
+    general = (bt != 0) & (bt != -np.inf)
+    ng = (Sq + 31) // 32
+    grp = np.zeros((B, H, ng), dtype=bool)
+    for g in range(ng):
+        grp[:, :, g] = general[:, :, 32 * g:32 * g + 32].any(axis=(-1, -2))
+    return grp[:, :, np.arange(Sq) // 32]
 
 
 def split_rows(B: int, H_total: int, Sq: int, n_full: int, heads=None, block_m: int = 128) -> np.ndarray:
@@ -468,7 +509,7 @@ def sage_forward(q, k, v, causal=False, sm_scale=None, block_n=32, out_dtype="bf
                      attn_mask=attn_mask, kv_split=kv_split)
 
 
-def sage_forward_varlen(q, k, v, cu_q, cu_k, causal=False, sm_scale=None, block_n=64, out_dtype="bf16"):
+def sage_forward_varlen(q, k, v, cu_q, cu_k, causal=False, sm_scale=None, block_n=32, out_dtype="bf16"):
     """Packed variable-length forward (src/sageattention/core.py:80-88: one call per sequence, NHD slices).
     q [total_q, H, D], k / v [total_k, Hkv, D] float32 arrays holding bf16 / fp16 values; cu_q / cu_k [batch + 1].
     Each sequence is quantized and attended on its own (sage_forward on its slices, bottom-right causal).  A sequence

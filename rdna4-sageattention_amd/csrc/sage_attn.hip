@@ -1,19 +1,22 @@
 // int8 QK^T / fp8 PV flash attention for gfx950 (CDNA4, wave64 MFMA).
 //
-// Math (the reference kernel's, kernel_build/make_sage.py:75-107, :196-237; make_sage_r2.py:54-269):
+// Math (the reference kernel's: kernel_build/make_sage.py:75-107, :196-237; make_sage_r2.py:52-269, 32-key tiles
+// per kernel_build/compile_attn.py:20):
 //   cl_i   = fp32(sm * log2e) * QS_i                      (sm = 1/sqrt(D) baked in; other scales folded into QS)
-//   S_ij   = sum_d Q8_id K8_jd                            (int32, exact; |S| < 2^21)
-//   rowmax = max over the tile's 32-key blocks of (max_j S_ij) * KS_block
-//   lazy rescale: m_cand = max(m, rowmax); need = (m_cand - m) * cl > 8; m_new = need ? m_cand : m
-//   p_ij   = exp2(fma(F_ij, ct, nk)) with F_ij = c + S_ij * 2^-26, ct = cl * KS_block * 2^26,
-//            nk = -(cl * m_new) - fp32(c * ct)       (<= 2^8, fits E4M3), c = fp32(1 / (2 pi)) = 0x3E22F983
-//            The QK accumulators start at the bit pattern of c, an inline constant of the MFMA (no registers
-//            hold the seed): since |S| < 2^21 the int32 result stays inside c's binade [1/8, 1/4), whose ulp is
-//            2^-26, so read as fp32 it is F exactly and needs no conversion; F * ct + nk equals
-//            S * ct - cl * m_new up to the rounding of nk.  The kernel keeps cl scaled by 2^26 and m by 2^-26
-//            (powers of two: every product and difference of the math above is the same bits, scaled).
-//   l      = corr * l + sum_j p_ij (fp32 p);  O = need ? O * corr : O;  O += e4m3(p) V8
+//   S_ij   = sum_d Q8_id K8_jd                            (int32, exact; |S| <= 127^2 * D)
+//   per 32-key block (one K scale KS_block each, make_sage_r2.py:141-190):
+//     rowmax = (max_j S_ij) * KS_block
+//     lazy rescale: m_cand = max(m, rowmax); need = (m_cand - m) * cl > 8; m_new = need ? m_cand : m
+//     p_ij   = exp2(fma(F_ij, ct, nk)) (<= 2^8, fits E4M3), ct = cl * KS_block
+//     l      = corr * l + sum_j p_ij (fp32 p);  O = need ? O * corr : O;  O += e4m3(p) V8;  corr = exp2((m - m_new) cl)
 //   out    = (O * ((1/448) / l)) * VS
+// Scores.  Head dims up to 128 seed the QK accumulators with the bit pattern of c = fp32(1 / (2 pi)) = 0x3E22F983,
+// an inline constant of the MFMA (no registers hold the seed): since -2,292,099 <= S < 6,097,183 there, the int32
+// result stays inside c's binade [1/8, 1/4), whose ulp is 2^-26, so read as fp32 it is F = c + S * 2^-26 exactly and
+// needs no conversion; nk = -(cl * m_new) - fp32(c * ct), so F * ct + nk equals S * ct - cl * m_new up to the
+// rounding of nk.  Those kernels keep cl scaled by 2^26 and m by 2^-26 (powers of two: every product and difference
+// of the math above is the same bits, scaled).  Head dim 256 reaches |S| = 4,129,024, outside that binade, so its
+// accumulators start at 0 and F = fp32(S) (v_cvt_f32_i32), nk = -(cl * m_new): the reference's arithmetic.
 //
 // gfx950 mapping.  A workgroup owns 128 query rows (4 waves x 32) of one (batch, head) and walks the KV sequence
 // in 64-key tiles staged in LDS (double buffered; the next tile's global loads are in flight while the current
@@ -74,15 +77,25 @@ template <int DT> __device__ __forceinline__ float mask_half_to_f32(uint32_t h) 
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// First QK MFMA of a key block: C = the bits of fp32(1 / (2 pi)) as the instruction's inline constant.  The
-// compiler folds a splat of it into the MFMA only where the splat has a single use; the second block's MFMA would
-// make it a 16-register value live through the whole tile loop, so that one is written out.  Its result is read
-// only as the exactly overlapping C operand of the block's next MFMA, which needs no wait states.
-__device__ __forceinline__ v16i mfma_i8_seeded(v4i a, v4i b) {
+// First QK MFMA of a key block: C = the seed as the instruction's inline constant (the bits of fp32(1 / (2 pi)),
+// or 0 for the unseeded head dim 256).  The compiler folds a splat of it into the MFMA only where the splat has a
+// single use; the second block's MFMA would make it a 16-register value live through the whole tile loop, so that
+// one is written out.  Its result is read only as the exactly overlapping C operand of the block's next MFMA, which
+// needs no wait states.
+template <bool SEEDED> __device__ __forceinline__ v16i mfma_i8_seeded(v4i a, v4i b) {
   v16i d;
-  asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494" : "=&v"(d) : "v"(a), "v"(b));
+  if constexpr (SEEDED)
+    asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494" : "=&v"(d) : "v"(a), "v"(b));
+  else
+    asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
   return d;
 }
+
+// Whether the QK accumulators of a kernel covering `da` channels start at the seed c = fp32(1 / (2 pi)).  The int32
+// sum read as fp32 is c + S * 2^-26 exactly while it stays inside c's binade [1/8, 1/4), i.e. for
+// -2,292,099 <= S < 6,097,183 (c = 10,680,707 * 2^-26).  |S| <= 127^2 * da: 1,032,256 (64), 1,548,384 (96, zero
+// padded), 2,064,512 (128) fit; head dim 256 reaches 4,129,024 and converts S with v_cvt_f32_i32 instead.
+__host__ __device__ constexpr bool attn_seeded(int da) { return 127 * 127 * da < 2292099; }
 
 constexpr int ATT_MAX_CHUNKS = 16;
 
@@ -128,6 +141,12 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   constexpr int KCH = D / 16;        // 16-byte chunks per K row
   constexpr int KLOADS = KTILE / 1024 / 4;  // 1 KiB direct loads per wave per tile (4 waves)
   constexpr int VLOADS = VTILE / 1024 / 4;
+  // Seeded scores (F = c + S * 2^-26, c = fp32(1 / (2 pi))): cl is kept scaled by 2^26 and m by 2^-26.  Unseeded
+  // (head dim 256): F = fp32(S) from v_cvt_f32_i32, no scaling, which is the reference's fp32(S) exactly.
+  constexpr bool SEEDED = attn_seeded(DA);
+  constexpr uint32_t SEED_BITS = SEEDED ? 0x3E22F983u : 0u;
+  constexpr float SEED_F = __builtin_bit_cast(float, SEED_BITS);
+  constexpr float SSCALE = SEEDED ? 67108864.0f : 1.0f;  // 2^26
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][TILE];
 
   // ---- work decode.  Dense: blocks [0, n_full) own whole query tiles (XCD-grouped); each later block owns one of
@@ -187,8 +206,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
 #pragma unroll
     for (int i = 0; i < NQK; ++i) qa[i] = *reinterpret_cast<const v4i*>(qp + 32 * i);
   }
-  // cl of the math scaled by 2^26, m in units of S * ks * 2^-26 (the seeded accumulators below hold S * 2^-26)
-  const float cl = (c0 * qs[qrow0 + qr]) * 67108864.0f;
+  // cl of the math scaled by SSCALE, m in units of S * ks / SSCALE (the seeded accumulators below hold S * 2^-26)
+  const float cl = (c0 * qs[qrow0 + qr]) * SSCALE;
   const float rcl = 1.0f / cl;  // the bias tiles keep m in S * ks * 2^-26 units
 
   // ---- KV range ----
@@ -276,13 +295,20 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
   float m = -INFINITY, l = 0.0f;
   v8i pb = {};  // E4M3 probabilities (B operand of the PV MFMA); each cvt rewrites one half, so no clearing
-  const v4i bw_none[4] = {};  // the bias argument of the tile bodies without an additive mask
+  v4i bw_none[4] = {};  // the bias argument of the tile bodies without an additive mask (never read)
 
   // One tile: S^T = K Q^T (int8 MFMA), online softmax with the reference's lazy rescale, O^T += V^T P^T (fp8 MFMA).
   // MODE 0: every key visible; 1: keys beyond the causal / padding bound masked; 2: keys whose bit of MW is clear
   // masked (MW = the lane's mask word of the tile); 3: the additive mask values BW (the lane's 32 16-bit values,
   // input dtype, -inf = masked) added in log2 units, with the row max taken over the biased logits.
-#define SAGE_TILE(T, MODE, MW, BW)                                                                         \
+  // The rescale decision is taken once per 32-key block, as the reference's 32-key tiles take it
+  // (kernel_build/make_sage_r2.py:180-190): block 0 against m, block 1 against the max m1 that block 0 left.  When no
+  // lane of the wave moves its max at block 1, one K = 64 PV MFMA per channel block adds both blocks (the reference's
+  // two PV steps up to the fp32 summation order).  Otherwise (rare: a row's max rising by 2^8 within a tile) the wave
+  // runs the tile body twice before the tile's barrier: pass 0 adds block 0 alone (block 1's bytes of the B operand
+  // cleared, m = m1), pass 1 (REDO) masks block 0 and adds block 1, whose rescale then comes before its MFMA.  No MFMA
+  // sits in a branch: the compiler loses the accumulators' coalescing around one and spills the whole loop.
+#define SAGE_TILE(T, MODE, MW, BW, REDO)                                                                       \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
     const uint8_t* kt_ = smem[t_ & 1];                                                                     \
@@ -292,12 +318,13 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       const v4i k0_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_]);                                         \
       const v4i k1_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_] + 32 * D);                                \
       s_[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0_, qa[i_], i_ == 0 ? seed16 : s_[0], 0, 0, 0);       \
-      s_[1] = i_ == 0 ? mfma_i8_seeded(k1_, qa[i_])                                                        \
+      s_[1] = i_ == 0 ? mfma_i8_seeded<SEEDED>(k1_, qa[i_])                                                \
                       : __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], s_[1], 0, 0, 0);                \
     }                                                                                                      \
     float sf_[2][16];                                                                                      \
     _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
-      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] = __int_as_float(s_[kb_][v_]);        \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_)                                                    \
+        sf_[kb_][v_] = SEEDED ? __int_as_float(s_[kb_][v_]) : (float)s_[kb_][v_];                          \
     if ((MODE) == 1) {                                                                                     \
       /* element (kb, v) holds key t * 64 + 4 hf + c with the constant c = 32 kb + 8 (v / 4) + v % 4; it is    \
          visible iff key <= min(Skv - 1, qr + off), i.e. c <= lim (one 32-bit bound per tile and lane) */   \
@@ -315,86 +342,152 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           sf_[kb_][v_] = __int_as_float((__float_as_int(sf_[kb_][v_]) & keep_) | (int)(0xFF800000u & ~(uint32_t)keep_)); \
         }                                                                                                  \
     }                                                                                                      \
+    if (REDO) {                                                                                            \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[0][v_] = -INFINITY;                            \
+    }                                                                                                      \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
-    bool need_;                                                                                            \
-    float mnew_, carg_, psum_ = 0.0f;                                                                      \
+    bool need0_, need1_;    /* block 0 / block 1 rescales */                                               \
+    float m1_, m2_;         /* the max after block 0 / after block 1 */                                    \
+    float carg0_, carg1_;   /* log2 of the rescale factors of the two blocks */                            \
+    float psum0_ = 0.0f, psum1_ = 0.0f;                                                                    \
     if ((MODE) == 3) {                                                                                     \
       /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))): the biased logit in log2 units (b = -inf for a masked \
-         key gives -inf); the lazy rescale compares its row max with m * cl and keeps m in S * ks * 2^-26      \
+         key gives -inf); the lazy rescale compares a block's max of t with m * cl and keeps m in S * ks      \
          units (m_new = m_cand * (1 / cl)) */                                                               \
-      const float ns0_ = -(SEED_F * ct0_), ns1_ = -(SEED_F * ct1_);                                        \
-      float tm_ = -INFINITY;                                                                               \
+      const float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;      \
+      float tm0_ = -INFINITY, tm1_ = -INFINITY;                                                            \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
           const uint32_t bw_ = (BW)[(16 * kb_ + v_) >> 3][((16 * kb_ + v_) >> 1) & 3];                     \
           const float b_ = mask_half_to_f32<OUT_DT>((v_ & 1) ? (bw_ >> 16) : (bw_ & 0xFFFFu));             \
           const float in_ = __builtin_fmaf(b_, 1.44269504088896341f, kb_ ? ns1_ : ns0_);                   \
           sf_[kb_][v_] = __builtin_fmaf(sf_[kb_][v_], kb_ ? ct1_ : ct0_, in_);                             \
-          tm_ = fmaxf(tm_, sf_[kb_][v_]);                                                                  \
+          if (kb_) tm1_ = fmaxf(tm1_, sf_[kb_][v_]);                                                       \
+          else tm0_ = fmaxf(tm0_, sf_[kb_][v_]);                                                           \
         }                                                                                                  \
-      tm_ = fmaxf(tm_, xor32_f32(tm_));                                                                    \
-      const float mc_ = m * cl;                                                                            \
-      const float mcand_ = fmaxf(mc_, tm_);                                                                \
-      need_ = (mcand_ - mc_) > 8.0f;                                                                       \
-      mnew_ = need_ ? mcand_ * rcl : m;                                                                    \
-      const float mref_ = mnew_ == -INFINITY ? 0.0f : mnew_;                                               \
-      carg_ = (m - mref_) * cl;                                                                            \
-      const float negl_ = 0.0f - cl * mref_;                                                               \
-      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
-        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
-          sf_[kb_][v_] = __builtin_amdgcn_exp2f(sf_[kb_][v_] + negl_);                                     \
-          psum_ += sf_[kb_][v_];                                                                           \
-        }                                                                                                  \
-    } else {                                                                                               \
-      /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose      \
-         int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */          \
-      int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                             \
-      _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                  \
-        mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                      \
-        mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                      \
+      tm0_ = fmaxf(tm0_, xor32_f32(tm0_));                                                                 \
+      tm1_ = fmaxf(tm1_, xor32_f32(tm1_));                                                                 \
+      const float mc0_ = m * cl;                                                                           \
+      const float mcand0_ = fmaxf(mc0_, tm0_);                                                             \
+      need0_ = (mcand0_ - mc0_) > 8.0f;                                                                    \
+      m1_ = need0_ ? mcand0_ * rcl : m;                                                                    \
+      const float mc1_ = m1_ * cl;                                                                         \
+      const float mcand1_ = fmaxf(mc1_, tm1_);                                                             \
+      need1_ = (mcand1_ - mc1_) > 8.0f;                                                                    \
+      m2_ = need1_ ? mcand1_ * rcl : m1_;                                                                  \
+      const float mref1_ = m1_ == -INFINITY ? 0.0f : m1_;                                                  \
+      const float mref2_ = m2_ == -INFINITY ? 0.0f : m2_;                                                  \
+      carg0_ = (m - mref1_) * cl;                                                                          \
+      carg1_ = (m1_ - mref2_) * cl;                                                                        \
+      const float negl1_ = 0.0f - cl * mref1_, negl2_ = 0.0f - cl * mref2_;                                \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
+        sf_[0][v_] = __builtin_amdgcn_exp2f(sf_[0][v_] + negl1_);                                          \
+        psum0_ += sf_[0][v_];                                                                              \
       }                                                                                                    \
-      const float mx0_ = __int_as_float(max(mi0_, xor32_i32(mi0_)));                                       \
-      const float mx1_ = __int_as_float(max(mi1_, xor32_i32(mi1_)));                                       \
-      const float rowmax_ = fmaxf((mx0_ - SEED_F) * ks0_, (mx1_ - SEED_F) * ks1_);                         \
-      const float mcand_ = fmaxf(m, rowmax_);                                                              \
-      need_ = (mcand_ - m) * cl > 8.0f;                                                                    \
-      mnew_ = need_ ? mcand_ : m;                                                                          \
+      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
+        sf_[1][v_] = __builtin_amdgcn_exp2f(sf_[1][v_] + negl2_);                                          \
+        psum1_ += sf_[1][v_];                                                                              \
+      }                                                                                                    \
+    } else {                                                                                               \
+      float mx0_, mx1_;                                                                                    \
+      if (SEEDED) {                                                                                        \
+        /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose    \
+           int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */        \
+        int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                           \
+        _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                \
+          mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                    \
+          mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                    \
+        }                                                                                                  \
+        mx0_ = __int_as_float(max(mi0_, xor32_i32(mi0_)));                                                 \
+        mx1_ = __int_as_float(max(mi1_, xor32_i32(mi1_)));                                                 \
+      } else {                                                                                             \
+        mx0_ = sf_[0][0];                                                                                  \
+        mx1_ = sf_[1][0];                                                                                  \
+        _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                \
+          mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                  \
+          mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                  \
+        }                                                                                                  \
+        mx0_ = fmaxf(mx0_, xor32_f32(mx0_));                                                               \
+        mx1_ = fmaxf(mx1_, xor32_f32(mx1_));                                                               \
+      }                                                                                                    \
+      /* the block's row max in m's units: fp32(max S * ks), scaled by 2^-26 when seeded (mx - c is exact) */ \
+      const float rm0_ = SEEDED ? (mx0_ - SEED_F) * ks0_ : mx0_ * ks0_;                                    \
+      const float rm1_ = SEEDED ? (mx1_ - SEED_F) * ks1_ : mx1_ * ks1_;                                    \
+      const float mcand0_ = fmaxf(m, rm0_);                                                                \
+      need0_ = (mcand0_ - m) * cl > 8.0f;                                                                  \
+      m1_ = need0_ ? mcand0_ : m;                                                                          \
+      const float mcand1_ = fmaxf(m1_, rm1_);                                                              \
+      need1_ = (mcand1_ - m1_) * cl > 8.0f;                                                                \
+      m2_ = need1_ ? mcand1_ : m1_;                                                                        \
       /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets  \
          from 0 instead of -inf keep corr and the exponents free of NaN */                                 \
-      const float mref_ = ((MODE) != 0 && mnew_ == -INFINITY) ? 0.0f : mnew_;                             \
-      carg_ = (m - mref_) * cl;                                                                            \
-      const float neg_ = 0.0f - cl * mref_;                                                                \
-      const float nk0_ = neg_ - SEED_F * ct0_, nk1_ = neg_ - SEED_F * ct1_;                                \
+      const float mref1_ = ((MODE) != 0 && m1_ == -INFINITY) ? 0.0f : m1_;                                \
+      const float mref2_ = ((MODE) != 0 && m2_ == -INFINITY) ? 0.0f : m2_;                                \
+      carg0_ = (m - mref1_) * cl;                                                                          \
+      carg1_ = (m1_ - mref2_) * cl;                                                                        \
+      /* p = exp2(fma(F, ct, nk)), nk = -(cl * m_new) - fp32(c * ct) (seeded) or -(cl * m_new) */           \
+      const float neg1_ = 0.0f - cl * mref1_, neg2_ = 0.0f - cl * mref2_;                                  \
+      const float nk0_ = SEEDED ? neg1_ - SEED_F * ct0_ : neg1_;                                           \
+      const float nk1_ = SEEDED ? neg2_ - SEED_F * ct1_ : neg2_;                                           \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
         sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, nk0_));                       \
-        psum_ += sf_[0][v_];                                                                               \
+        psum0_ += sf_[0][v_];                                                                              \
       }                                                                                                    \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
         sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, nk1_));                       \
-        psum_ += sf_[1][v_];                                                                               \
+        psum1_ += sf_[1][v_];                                                                              \
       }                                                                                                    \
     }                                                                                                      \
-    /* corr = exp2(carg): 1 in a lane whose max did not move (carg = 0), so the exponential is taken only in   \
-       the rare tiles in which some lane of the wave rescales */                                            \
+    /* slow: some lane moves its max at block 1 in a first pass, which then adds block 0 alone */          \
+    const bool slow_ = !(REDO) && __ballot(need1_) != 0;                                                   \
+    /* the rescale before this pass's MFMA: exp2(carg0 + carg1) with carg1 counted unless slow; one of the    \
+       two is 0 wherever a row has seen a key (a non-slow first pass has no block-1 rescale, a redo pass's    \
+       masked block 0 none at block 0), so this is the reference's corr0 or corr1.  Taken only in the rare    \
+       passes in which some lane of the wave rescales (elsewhere it is exp2(0) = 1). */                       \
     float corr_ = 1.0f;                                                                                    \
-    if (__ballot(need_) != 0) {                                                                            \
-      corr_ = __builtin_amdgcn_exp2f(carg_);                                                               \
+    if (__ballot(need0_ || (!slow_ && need1_)) != 0) {                                                     \
+      corr_ = __builtin_amdgcn_exp2f(carg0_ + (slow_ ? 0.0f : carg1_));                                    \
       _Pragma("unroll") for (int i_ = 0; i_ < NPV; ++i_)                                                   \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) o[i_][v_] *= corr_;                              \
     }                                                                                                      \
-    l = corr_ * l + psum_;                                                                                 \
-    m = mnew_;                                                                                             \
+    l = (corr_ * l + psum0_) + (slow_ ? 0.0f : psum1_);                                                    \
+    m = slow_ ? m1_ : m2_;                                                                                 \
     _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                     \
       const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                         \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);        \
+    }                                                                                                      \
+    /* bytes 16-31 of the B operand are block 1's keys (the V8T key order) */                               \
+    if (slow_) {                                                                                           \
+      pb[4] = 0;                                                                                           \
+      pb[5] = 0;                                                                                           \
+      pb[6] = 0;                                                                                           \
+      pb[7] = 0;                                                                                           \
     }                                                                                                      \
     _Pragma("unroll") for (int j_ = 0; j_ < NPV; ++j_) {                                                   \
       const v4i a0_ = *reinterpret_cast<const v4i*>(vt_ + vo0 + j_ * 32 * BN);                             \
       const v4i a1_ = *reinterpret_cast<const v4i*>(vt_ + vo1 + j_ * 32 * BN);                             \
       const v8i va_ = {a0_[0], a0_[1], a0_[2], a0_[3], a1_[0], a1_[1], a1_[2], a1_[3]};                    \
       o[j_] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va_, pb, o[j_], 0, 0, 0, 0, 0, 0);           \
+    }                                                                                                      \
+    redo_ = slow_;                                                                                         \
+  } while (0)
+
+  // The tile's passes: one, or two when some lane of the wave moves its max at block 1 (the body sets redo_).  The
+  // memory clobber keeps the LDS operand reads inside the loop, and the tile's mask word and bias values pass through
+  // empty asm statements on every pass so that nothing derived from them (32 bit masks, 32 scaled biases) is hoisted
+  // out of the loop and held across the whole body.
+#define SAGE_TILE_PASSES(T, MODE, MW, BW)                                                                   \
+  do {                                                                                                     \
+    bool redo_ = false;                                                                                    \
+    _Pragma("nounroll") for (int pass_ = 0;; ++pass_) {                                                    \
+      asm volatile("" ::: "memory");                                                                       \
+      uint32_t mwp_ = (MW);                                                                                \
+      if ((MODE) == 2) asm volatile("" : "+v"(mwp_));                                                      \
+      if ((MODE) == 3) asm volatile("" : "+v"((BW)[0]), "+v"((BW)[1]), "+v"((BW)[2]), "+v"((BW)[3]));      \
+      SAGE_TILE(T, MODE, mwp_, BW, pass_ > 0);                                                             \
+      if (!redo_) break;                                                                                   \
     }                                                                                                      \
   } while (0)
 
@@ -405,9 +498,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   if (CAUSAL) t_mask = min(t_mask, max(0, (q0 + off + 1) / BN));
   t_mask = min(t_mask, t_hi);
   // QK accumulators start at the bits of c = fp32(1 / (2 pi)) (0x3E22F983, which the compiler encodes as the
-  // MFMA's inline constant): the int32 sum read as fp32 is c + S * 2^-26, exactly
-  constexpr uint32_t SEED_BITS = 0x3E22F983u;
-  constexpr float SEED_F = __builtin_bit_cast(float, SEED_BITS);
+  // MFMA's inline constant): the int32 sum read as fp32 is c + S * 2^-26, exactly; unseeded kernels start at 0
   v16i seed16;
 #pragma unroll
   for (int v = 0; v < 16; ++v) seed16[v] = (int)SEED_BITS;
@@ -430,7 +521,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           c_nxt = mcls[t + 1];
           SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
         }
-        if (c_cur == 1) SAGE_TILE(t, 0, 0u, bw_none);
+        if (c_cur == 1) SAGE_TILE_PASSES(t, 0, 0u, bw_none);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
@@ -448,7 +539,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
             c_nxt = mcls[t + 1];
             SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
           }
-          SAGE_TILE(t, 2, mw_cur, bw_none);
+          SAGE_TILE_PASSES(t, 2, mw_cur, bw_none);
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           asm volatile("" ::"v"(mw_nxt));
           __syncthreads();
@@ -467,7 +558,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
         const int tn_ = min(t + 1, t_hi - 1);
         c_nxt = mcls[tn_];
         SAGE_ISSUE_TILE(tn_, (t + 1) & 1);
-        SAGE_TILE(t, 3, 0u, bias_w);
+        SAGE_TILE_PASSES(t, 3, 0u, bias_w);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
@@ -475,19 +566,20 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   } else {
     for (; t < t_mask; ++t) {
       if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
-      SAGE_TILE(t, 0, 0u, bw_none);
+      SAGE_TILE_PASSES(t, 0, 0u, bw_none);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     }
     for (; t < t_hi; ++t) {
       if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
-      SAGE_TILE(t, 1, 0u, bw_none);
+      SAGE_TILE_PASSES(t, 1, 0u, bw_none);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
     }
   }
 #undef SAGE_ISSUE_TILE
 #undef SAGE_TILE
+#undef SAGE_TILE_PASSES
 
   // ---- epilogue ----
   const float lt = l + xor32_f32(l);
@@ -507,7 +599,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     const int64_t units = (int64_t)(total - n_full) * chunks;
     if (hf == 0)
       reinterpret_cast<float2*>(reinterpret_cast<uint8_t*>(part) + ws_ml_offset(units, D))[(int64_t)unit * ATT_BM + q] =
-          make_float2(m * 67108864.0f, lt);  // m in S * ks units, as the merge kernel's cl expects
+          make_float2(m * SSCALE, lt);  // m in S * ks units, as the merge kernel's cl expects
     return;
   }
   const float inv = lt > 0.0f ? (1.0f / 448.0f) / lt : 0.0f;  // a row without any visible key is written as 0

@@ -1,12 +1,12 @@
 """gfx950 attention kernel vs the CPU emulation of the reference's quantized math and vs float attention.
 
-Tolerances (north star): max |out - emulation| <= 2e-2 with the emulation run at the kernel's own 64-key tile, and
-cosine >= 0.999 against float attention; the reference's own gate is cosine > 0.998 (tests/test_attention.py:175).
-Beyond the north star, the kernel follows the emulation element by element: the exp2 implementation and the fp32
-summation order inside the PV MFMA are the only differences, so most output elements are the emulation's bits and the
-rest move by a probability whose E4M3 rounding flipped.  Measured on these cases: 98.5-99% (bf16) and 91-95% (fp16)
-of the elements bit-identical, the largest difference 0.4% of the largest |output|; the test asserts >= 95% / 85%
-and 1%.
+Tolerances (north star): max |out - emulation| <= 2e-2 with the emulation taking the reference's lazy-rescale
+decisions once per 32-key block (kernel_build/compile_attn.py:20), and cosine >= 0.999 against float attention; the
+reference's own gate is cosine > 0.998 (tests/test_attention.py:54).  Beyond the north star, the kernel follows the
+emulation element by element: the exp2 implementation and the fp32 summation order inside the PV MFMA are the only
+differences, so most output elements are the emulation's bits and the rest move by a probability whose E4M3 rounding
+flipped.  The test asserts >= 95% (bf16) / 85% (fp16) of the elements bit-identical and the largest difference within
+1% of the largest |output|.
 """
 import numpy as np
 import pytest
@@ -55,11 +55,12 @@ def _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=0):
 
 
 def _emulate(q, k, v, layout, causal, sm_scale=None, out_dtype="bf16", split=None):
-    """Emulation at the kernel's 64-key tile, following the kernel's split plan (`split`, from gpu_util.kv_split)."""
+    """Emulation with the reference's 32-key rescale blocks, following the kernel's split plan (`split`, from
+    gpu_util.kv_split)."""
     qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
     q8, qs = orc.quant_q(qn, sm_scale)
     k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(kn.shape[2]))
-    emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=64, out_dtype=out_dtype,
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=32, out_dtype=out_dtype,
                         kv_split=split)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, sm_scale=sm_scale)
     return emu, ref

@@ -17,7 +17,7 @@ from oracle import sage_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-MAX_ABS = 2e-2   # vs the oracle's emulation at the kernel's 64-key tile
+MAX_ABS = 2e-2   # vs the oracle's emulation with the reference's 32-key rescale blocks
 COS = 0.999      # vs float64 attention
 
 
@@ -109,7 +109,7 @@ def _check_against_separate_calls(q, k, v, cu_q, cu_k, causal, r):
 
 def _check_against_oracle(q, k, v, cu_q, cu_k, causal, out, out_dtype):
     emu = orc.sage_forward_varlen(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q, cu_k,
-                                  causal=causal, block_n=64, out_dtype=out_dtype)
+                                  causal=causal, block_n=32, out_dtype=out_dtype)
     got = out.float().cpu().numpy()
     rows = ~np.isnan(emu[:, 0, 0])
     assert float(np.abs(got[rows] - emu[rows]).max()) <= MAX_ABS
