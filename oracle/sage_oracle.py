@@ -266,7 +266,7 @@ def logit_scale_base(d: int) -> np.float32:
 
 def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n: int = 32,
               out_dtype: str = "bf16", threshold: float = RESCALE_THRESHOLD, return_stats: bool = False,
-              kv_split=None, attn_mask=None):
+              kv_split=None, attn_mask=None, q_rows=None, seq_q=None):
     """Quantized attention as the reference kernel computes it.
 
     q8 [B, H, Sq, D] int8, qs [B, H, Sq] f32, k8 [B, Hkv, Sp, D] int8, ks [B, Hkv, Sp/32] f32,
@@ -287,7 +287,11 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     array is an additive mask (SDPA: softmax(Q K^T * scale + mask), -inf = masked), emulated as the gfx950 kernel
     runs it: per 32-row group (a wave) and key tile whose values are all 0 or -inf, the boolean path above; otherwise
     the bias path of ``_online_softmax``.  The group-and-tile classes are per 32 rows and 64 keys (the kernel's tile),
-    whatever ``block_n``."""
+    whatever ``block_n``.
+
+    ``q_rows`` (int array, with ``seq_q``): the query axis of q8 / qs holds only these rows of a query sequence of
+    length seq_q (a sample of a long problem; the bottom-right causal mask and ``kv_split`` rows refer to these
+    positions).  Not combined with ``attn_mask``."""
     B, H, Sq, D = q8.shape
     Hkv = k8.shape[1]
     assert block_n % KV_BLOCK == 0 and KERNEL_TILE % block_n == 0 and H % Hkv == 0
@@ -306,11 +310,16 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
             attn_mask = np.broadcast_to(attn_mask, (B, H, q8.shape[2], seq_kv))
         else:
             attn_mask = np.broadcast_to(attn_mask.astype(F32), (B, H, q8.shape[2], seq_kv))
-    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask)
+    if q_rows is not None:
+        assert attn_mask is None and seq_q is not None and len(q_rows) == q8.shape[2]
+        qpos = (np.asarray(q_rows, dtype=np.int64), int(seq_q))
+    else:
+        qpos = (np.arange(q8.shape[2]), q8.shape[2])
+    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask, qpos)
     if kv_split is not None:
         chunks, rows = kv_split
         parts = [_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold,
-                                 *krange(c, chunks), attn_mask)
+                                 *krange(c, chunks), attn_mask, qpos)
                  for c in range(chunks)]
         mm = parts[0][1]
         for _, mc, _ in parts[1:]:
@@ -339,9 +348,11 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     return out
 
 
-def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi, attn_mask=None):
+def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi, attn_mask=None,
+                    qpos=None):
     """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row.  attn_mask:
-    None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).
+    None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).  qpos:
+    (the rows' positions in the query sequence, its length), default all Sq rows.
 
     Bias path (float masks, tiles of a 32-row group holding a value other than 0 and -inf), in log2 units:
     t = fma(F, ct', fma(b, log2e, -fp32(c * ct'))) per score (F = c + S * 2^-26, ct' = ct * 2^26, c the seed; for
@@ -356,8 +367,8 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
     m = np.full((B, H, Sq), -np.inf, dtype=F32)
     l = np.zeros((B, H, Sq), dtype=F32)
     o = np.zeros((B, H, Sq, D), dtype=F32)
-    rows = np.arange(Sq)
-    causal_off = seq_kv - Sq
+    rows, seq_q = qpos if qpos is not None else (np.arange(Sq), Sq)   # query positions, query length
+    causal_off = seq_kv - seq_q
     nsub = block_n // KV_BLOCK
     for t in range(t_lo, t_hi):
         j0 = t * block_n

@@ -26,8 +26,9 @@ from ._attention import attention as _attention_impl
 __all__ = ["sageattn", "attention", "attention_varlen", "lse", "is_available", "Unsupported", "ARCHS", "HEAD_DIMS"]
 __version__ = "0.1.0"
 
-# The C binding behind F.scaled_dot_product_attention.  Apps that replace F.scaled_dot_product_attention with
-# sageattn would otherwise recurse through the fallback (reference CHANGELOG 2.2.0+rdna4.0.2.1).
+# Fallbacks call torch's C entry point of SDPA directly: a caller may have monkey-patched
+# F.scaled_dot_product_attention to point at sageattn, and the Python-level function would then lead straight back
+# here (reference CHANGELOG 2.2.0+rdna4.0.2.1).
 _torch_sdpa = torch._C._nn.scaled_dot_product_attention
 
 
@@ -38,8 +39,8 @@ def _env_int(names, default):
     return default
 
 
-# Calls below these sizes run torch SDPA: the fixed quantization pass costs more than int8 attention saves.
-# CDNA4_SAGE_* take precedence; the reference's RDNA4_SAGE_* names are honoured for drop-in callers.
+# Size thresholds of the kernel route: below them the quantization pass and launches cost more than the int8 / fp8
+# products save, and SDPA runs.  CDNA4_SAGE_* override; the reference's RDNA4_SAGE_* names are read as well.
 MIN_WORK = _env_int(("CDNA4_SAGE_MIN_WORK", "RDNA4_SAGE_MIN_WORK"), 64 * 2**20)  # batch * heads * q_len * kv_len
 MIN_KV = _env_int(("CDNA4_SAGE_MIN_KV", "RDNA4_SAGE_MIN_KV"), 1024)
 # attn_masks (bool, or additive of q's dtype) run on the kernel (quantized like every other call); 0 restores the
@@ -57,9 +58,12 @@ def is_available(device=None) -> bool:
 
 def _plain_eager(*ts) -> bool:
     """True for an eager call on plain tensors: no torch.compile / export tracing, no tensor subclass (fake or
-    functional tensors) and no active dispatch mode (make_fx and the like).  Such calls may run the op's implementation
-    directly; anything else goes through the registered op."""
+    functional tensors), no active dispatch mode (make_fx and the like) and no autograd recording on the inputs.  Such
+    calls may run the op's implementation directly; anything else goes through the registered op, so that tracers see
+    its fake implementation and autograd sees an op without a derivative (backward raises, as in the reference)."""
     if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
+        return False
+    if torch.is_grad_enabled() and any(t.requires_grad for t in ts):
         return False
     return all(type(t) is torch.Tensor for t in ts)
 
@@ -86,7 +90,8 @@ def _sdpa(q, k, v, tensor_layout, is_causal, sm_scale, attn_mask):
     gqa = q.shape[1] != k.shape[1]
     Sq, Skv = q.shape[2], k.shape[2]
     if is_causal and (Sq != Skv or attn_mask is not None):
-        # SageAttention / FlashAttention semantics: bottom-right aligned causal mask
+        # with q_len != kv_len (or a mask to combine) the causal triangle is anchored at the last key, the convention
+        # SageAttention and FlashAttention use, which SDPA's is_causal flag does not follow
         causal = causal_lower_right(Sq, Skv)._materialize(q.device)
         if attn_mask is None:
             attn_mask = causal

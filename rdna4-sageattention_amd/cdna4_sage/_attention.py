@@ -222,6 +222,10 @@ def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
         raise Unsupported("empty or too large")
     if is_causal and Sq > Skv:
         raise Unsupported("causal LSE needs q_len <= kv_len")
+    if sm_scale is not None and not sm_scale > 0:
+        # the reference's _lse takes an explicit scale as given (src/sageattention/core.py:30); the kernel's 0 means
+        # the default 1 / sqrt(head_dim), so such scales go to the torch formula
+        raise Unsupported("sm_scale <= 0")
     q, sq_ = _bsh(q, layout)
     k, sk_ = _bsh(k, layout)
     out = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)

@@ -1,13 +1,13 @@
 """ComfyUI attention backend on the gfx950 kernels.
 
     import cdna4_sage.comfy
-    cdna4_sage.comfy.register()   # adds "cdna4_sage" to ComfyUI's attention registry
+    cdna4_sage.comfy.register()   # ComfyUI's attention registry now lists "cdna4_sage"
 
-Then select it per model through transformer_options["optimized_attention_override"] or preferred_attention="cdna4_sage",
-like any registered backend (reference: src/rdna4_sage/comfy.py:14-40, which registers "rdna4_sage"; that name is
-registered by rdna4_sage.comfy.register()).  Calls with a mask or with low_precision_attention=False go to ComfyUI's
-own PyTorch attention; everything else goes through cdna4_sage.sageattn, whose router sends small or unsupported
-shapes to SDPA.
+A workflow picks a registered backend by name, per model (transformer_options["optimized_attention_override"]) or
+as the preferred one (preferred_attention="cdna4_sage").  The reference registers the same function as "rdna4_sage"
+(src/rdna4_sage/comfy.py:14-40); rdna4_sage.comfy.register() does that here.  Masked calls and calls with
+low_precision_attention=False stay on ComfyUI's own PyTorch attention; the rest go through cdna4_sage.sageattn, whose
+router sends small or unsupported shapes to SDPA.
 """
 from comfy.ldm.modules.attention import attention_pytorch, register_attention_function, wrap_attn
 

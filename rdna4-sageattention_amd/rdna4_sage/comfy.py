@@ -1,4 +1,4 @@
-"""ComfyUI backend under the reference's import and registry name (src/rdna4_sage/comfy.py:1-45):
+"""ComfyUI backend under the reference's import and registry name (src/rdna4_sage/comfy.py:1-40):
 
     import rdna4_sage.comfy
     rdna4_sage.comfy.register()   # registers "rdna4_sage", backed by the gfx950 kernels

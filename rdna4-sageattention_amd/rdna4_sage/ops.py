@@ -7,7 +7,8 @@ from cdna4_sage import ops as _ops
 
 @torch.library.custom_op("rdna4_sage::attention", mutates_args=())
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout: str, sm_scale: float, is_causal: bool) -> torch.Tensor:
-    """Returns (B, Sq, H, D) contiguous. sm_scale <= 0 selects 1/sqrt(head_dim)."""
+    """Output [batch, q_len, heads, head_dim], contiguous, whatever the input layout; a non-positive sm_scale stands
+    for the default 1 / sqrt(head_dim)."""
     return _ops._impl(q, k, v, layout, sm_scale, is_causal)
 
 

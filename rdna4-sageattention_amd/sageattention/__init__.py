@@ -1,6 +1,6 @@
-"""SageAttention 2.2 drop-in for AMD MI355X (gfx950), backed by cdna4_sage.
+"""The `sageattention` package name for MI355X (gfx950): installs in place of SageAttention 2.2 and exports the same
+seven entry points (reference: src/sageattention/__init__.py:6-13), all running on cdna4_sage's kernels.
 
-Same import paths and functions as SageAttention 2.2 (reference: src/sageattention/__init__.py:1-13):
     from sageattention import sageattn
 """
 from .core import sageattn, sageattn_varlen

@@ -66,10 +66,11 @@ def sageattn(
     return_lse: bool = False,
     **kwargs: Any,
 ):
-    """Attention for [B, H, L, D] ("HND") or [B, L, H, D] ("NHD") fp16 / bf16 tensors; returns the input layout and
-    dtype, plus the row logsumexp [B, H, q_len] when return_lse is True.  Causal masks are bottom-right aligned.
-    There is no attn_mask parameter (ComfyUI reads the signature); a mask passed as a keyword (bool, or additive of
-    the inputs' dtype) runs on the kernel.  The LSE, as the reference's, ignores the mask."""
+    """q / k / v of dtype fp16 or bf16, laid out "HND" [batch, heads, tokens, head_dim] or "NHD" [batch, tokens,
+    heads, head_dim].  The result keeps that layout and dtype; return_lse=True adds the fp32 logsumexp of every query
+    row, [batch, heads, q_len].  A causal mask aligns the last query with the last key.  attn_mask is read from the
+    keyword arguments only (ComfyUI inspects this signature and expects no such parameter); bool masks and additive
+    ones of the inputs' dtype run on the kernel.  The logsumexp ignores any mask, as the reference's does."""
     if (return_lse and q.is_cuda and not torch.compiler.is_compiling()
             and not torch.cuda.is_current_stream_capturing()):
         # the LSE pass does not depend on the attention: it runs on a side stream (default priority) concurrently with
@@ -117,8 +118,10 @@ def sageattn_varlen(
     smooth_k: bool = True,
     **kwargs: Any,
 ) -> torch.Tensor:
-    """Packed variable-length attention: q [total_q, H, D], k / v [total_k, Hkv, D], cu_seqlens [batch + 1]
-    (reference: src/sageattention/core.py:66-89, a host loop of sageattn calls after reading cu_seqlens back).
+    """Sequences packed along the token axis: q is [sum of query lengths, heads, head_dim], k and v
+    [sum of key lengths, kv heads, head_dim]; cu_seqlens_q / cu_seqlens_k hold the batch + 1 sequence offsets
+    (reference: src/sageattention/core.py:66-89, which loops over the sequences on the host after reading the
+    offsets back).
     On gfx950, when the longest key sequence reaches the kernel's minimum length (max_seqlen_k >= MIN_KV, or unknown),
     the whole batch runs in one stream-ordered pass of the int8/fp8 kernels with per-sequence scales and no host
     synchronisation; sequences that a per-sequence call would send to SDPA for being short are quantized there too.

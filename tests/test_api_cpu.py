@@ -257,3 +257,34 @@ def test_single_block_layouts(monkeypatch, B, H, Hkv, Sq, Skv, D):
     assert all(e <= o for e, o in zip(vends, voffs[1:])) and vends[-1] <= vtotal
     _attention._forward_layout.cache_clear()
     _attention._varlen_layout.cache_clear()
+
+
+def test_autograd_inputs_reach_the_registered_op(monkeypatch):
+    """With inputs that require grad, the Python entry points go through the registered op (not the eager shortcut),
+    whose output autograd tracks; backward then raises for the missing derivative, as for the reference's op."""
+    from cdna4_sage import ops
+
+    q = torch.randn(1, 2, 16, 64, dtype=torch.bfloat16, requires_grad=True)
+    k = torch.randn(1, 2, 16, 64, dtype=torch.bfloat16)
+    assert not cdna4_sage._plain_eager(q, k, k)
+    with torch.no_grad():
+        assert cdna4_sage._plain_eager(q, k, k)
+    calls = []
+    monkeypatch.setattr(ops, "_impl", lambda q_, k_, v_, layout, sm, causal: calls.append(1) or
+                        torch.zeros(q_.shape[0], q_.shape[2], q_.shape[1], q_.shape[3], dtype=q_.dtype))
+    monkeypatch.setattr(cdna4_sage, "_attention_impl", lambda *a, **kw: pytest.fail("eager shortcut taken"))
+    out = cdna4_sage.attention(q, k, k, "HND")
+    assert calls and out.requires_grad
+    with pytest.raises(RuntimeError):
+        out.float().sum().backward()
+
+
+def test_lse_with_non_positive_sm_scale_uses_it_as_given():
+    """The reference's _lse multiplies by an explicit sm_scale as given (src/sageattention/core.py:30), 0 and negative
+    values included; the LSE kernel entry leaves such scales to the torch formula."""
+    q = _rand((1, 2, 20, 64), 31)
+    k = _rand((1, 2, 40, 64), 32)
+    for sm in (0.0, -0.1):
+        lse = sageattention.core._lse(q, k, "HND", False, sm)
+        s = torch.matmul(q.double(), k.double().transpose(-1, -2)) * sm
+        torch.testing.assert_close(lse.double(), torch.logsumexp(s, -1), atol=2e-3, rtol=1e-4)

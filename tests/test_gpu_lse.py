@@ -93,3 +93,18 @@ def test_return_lse_side_stream_joins_the_callers_stream(dev):
     s.synchronize()
     torch.testing.assert_close(lse_copy, ref_lse, atol=0, rtol=0)
     torch.testing.assert_close(out_copy, ref_out.float(), atol=0, rtol=0)
+
+
+def test_return_lse_with_non_positive_sm_scale_uses_it_as_given(dev):
+    """An explicit sm_scale <= 0 is taken as given by the reference's _lse (src/sageattention/core.py:30): the LSE
+    kernel entry refuses it and the torch formula computes it, 0 giving log(kv_len)."""
+    q, k = _inputs(1, 2, 2, 300, 1100, 128, torch.bfloat16, "HND", seed=9)
+    qd, kd = q.to(dev), k.to(dev)
+    with pytest.raises(cdna4_sage.Unsupported):
+        cdna4_sage.lse(qd, kd, "HND", 0.0, False)
+    for sm in (0.0, -0.05):
+        _, lse = sageattention.sageattn(qd, kd, kd, tensor_layout="HND", sm_scale=sm, return_lse=True)
+        s = torch.matmul(q.double(), k.double().transpose(-1, -2)) * sm
+        torch.testing.assert_close(lse.cpu().double(), torch.logsumexp(s, -1), atol=2e-3, rtol=1e-4)
+    _, lse0 = sageattention.sageattn(qd, kd, kd, tensor_layout="HND", sm_scale=0.0, return_lse=True)
+    torch.testing.assert_close(lse0.cpu(), torch.full((1, 2, 300), float(np.log(1100.0))), atol=1e-4, rtol=0)

@@ -516,3 +516,102 @@ def test_lse_reference_matches_torch_logsumexp():
         if causal:
             sc.masked_fill_(torch.ones(50, 80, dtype=torch.bool).tril(80 - 50).logical_not(), float("-inf"))
         assert np.allclose(got, torch.logsumexp(sc, -1).numpy(), atol=1e-10)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# The lazy rescale and the E4M3 probabilities, on hand-made quantized operands (one query, 64 keys, head dim 64):
+# q8 = e_0, k8[j] = s_j e_0, so S_j = s_j; KS = 1 and QS chosen so that cl = fp32(1/8): key j's logit is s_j / 8
+# in log2 units.  V is one-hot (key j -> channel j, V8 = 448, VS = 1), so out_c * l = p8_c, the E4M3 probability
+# the PV product used for key c.
+# ---------------------------------------------------------------------------------------------------------------
+CL_HANDMADE = 1.0 / 8
+
+
+def _handmade(s_keys):
+    d = 64
+    q8 = np.zeros((1, 1, 1, d), dtype=np.int8)
+    q8[..., 0] = 1
+    k8 = np.zeros((1, 1, d, d), dtype=np.int8)
+    k8[0, 0, :, 0] = np.asarray(s_keys, dtype=np.int64)
+    ks = np.ones((1, 1, 2), dtype=np.float32)
+    qs = np.full((1, 1, 1), np.float32(CL_HANDMADE) / orc.logit_scale_base(d), dtype=np.float32)
+    v8 = np.zeros((1, 1, d, d), dtype=np.uint8)
+    v8[0, 0, np.arange(d), np.arange(d)] = orc.f32_to_e4m3(np.array([448.0], dtype=np.float32))[0]
+    vs = np.ones((1, 1, d), dtype=np.float32)
+    return q8, qs, k8, ks, v8, vs
+
+
+def _p8(s_keys, **kw):
+    q8, qs, k8, ks, v8, vs = _handmade(s_keys)
+    out, m, l = orc.attention(q8, qs, k8, ks, v8, vs, 64, out_dtype="f32", return_stats=True, **kw)
+    return out[0, 0, 0].astype(np.float64) * float(l[0, 0, 0]), float(m[0, 0, 0])
+
+
+def test_lazy_rescale_keeps_stale_max_below_threshold_and_moves_above():
+    """Block 0's max sets m (key 0, logit 1); block 1's key 40 rises by 5 log2 units: below the threshold of 8
+    (make_sage_r2.py:185-187) the max stays stale, so key 40's probability is 2^5 and enters the PV product as
+    E4M3(32) = 32; a rise of 10 moves the max to key 40 (probability 1).  A threshold other than 8 between 5 and 10,
+    or a decision over the 64-key tile instead of per 32-key block, fails one of the two."""
+    s = np.zeros(64, dtype=np.int64)
+    s[0] = 8
+    s[40] = 8 * 6
+    p8, m = _p8(s)
+    assert m == 8.0                                    # stale: block 0's max (S * KS units)
+    assert abs(p8[40] - 32.0) < 1e-4 and abs(p8[0] - 1.0) < 1e-6
+    s[40] = 8 * 11
+    p8, m = _p8(s)
+    assert m == 88.0                                   # moved to key 40
+    assert abs(p8[40] - 1.0) < 1e-6
+    # the per-block decision is what keeps the max stale: one decision over the 64-key tile moves it at once
+    s[40] = 8 * 6
+    p8_64, m64 = _p8(s, block_n=64)
+    assert m64 == 48.0 and abs(p8_64[40] - 1.0) < 1e-6
+
+
+def test_probabilities_entering_pv_are_e4m3():
+    """Every probability that reaches the PV product is an E4M3 value (make_sage_r2.py:208-214 pack P to fp8); the
+    float probabilities of these keys are not, so an emulation that dropped the rounding fails."""
+    rng = np.random.default_rng(5)
+    s = rng.integers(-60, 61, size=64)
+    p8, m = _p8(s)
+    e4 = orc.e4m3_to_f32(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    e4 = np.unique(e4[np.isfinite(e4)])
+    nearest = e4[np.abs(p8[:, None] - e4[None, :]).argmin(1)]
+    assert (np.abs(p8 - nearest) <= 1e-5 * np.maximum(np.abs(nearest), 1e-3)).all()
+    # the unrounded probabilities (relative to the same max) are mostly not E4M3 values
+    p = np.exp2((s - m) * float(np.float32(CL_HANDMADE)))
+    near_p = e4[np.abs(p[:, None] - e4[None, :]).argmin(1)]
+    assert (np.abs(p - near_p) > 1e-3 * p).mean() > 0.8
+
+
+def test_block32_and_block64_decisions_differ():
+    """With a rise of 5.25 log2 units in block 1 the 32-key decisions keep the stale max (p8 = E4M3(2^5.25) = 40)
+    and the 64-key decision does not (key 0 gets E4M3(2^-5.25) = 13 * 2^-9): the normalised outputs differ, so a
+    gate at block_n 32 distinguishes the two."""
+    s = np.zeros(64, dtype=np.int64)
+    s[0] = 8
+    s[40] = 8 + 42                                     # 42 / 8 = 5.25 log2 units above key 0
+    q8, qs, k8, ks, v8, vs = _handmade(s)
+    o32 = orc.attention(q8, qs, k8, ks, v8, vs, 64, out_dtype="f32", block_n=32)
+    o64 = orc.attention(q8, qs, k8, ks, v8, vs, 64, out_dtype="f32", block_n=64)
+    p8, _ = _p8(s)
+    assert abs(p8[40] - 40.0) < 1e-4
+    assert not np.array_equal(o32, o64)
+    assert abs(o32[0, 0, 0, 40] / o32[0, 0, 0, 0] - 40.0) < 1e-4
+    assert abs(o64[0, 0, 0, 40] / o64[0, 0, 0, 0] - 512.0 / 13.0) < 1e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_on_sampled_query_rows(causal):
+    """q_rows / seq_q: the emulation of a subset of query rows equals those rows of the whole emulation bit for bit
+    (causal offsets and split rows refer to the rows' positions)."""
+    q, k, v = _bf16((1, 2, 200, 64), 60), _bf16((1, 2, 260, 64), 61), _bf16((1, 2, 260, 64), 62)
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v)
+    rows_split = np.zeros((1, 2, 200), dtype=bool)
+    rows_split[:, 1, 128:] = True
+    full = orc.attention(q8, qs, k8, ks, v8, vs, 260, causal=causal, kv_split=(3, rows_split))
+    sel = np.r_[0:10, 120:140, 190:200]
+    part = orc.attention(np.ascontiguousarray(q8[:, :, sel]), np.ascontiguousarray(qs[:, :, sel]), k8, ks, v8, vs,
+                         260, causal=causal, kv_split=(3, rows_split[:, :, sel]), q_rows=sel, seq_q=200)
+    assert np.array_equal(part, full[:, :, sel])
