@@ -10,7 +10,8 @@
  *
  * Conventions
  *  - Return value: SAGE_OK (0) or a SAGE_ERR_* code; sage_last_error() gives the message (thread-local).
- *  - Memory: the caller owns every buffer (inputs, outputs, intermediates).  The library allocates nothing.
+ *  - Memory: the caller owns every buffer (inputs, outputs, intermediates) and the library allocates nothing at run
+ *    time; its only device memory is the static scratch array of sage_forward_noalloc (one per GPU it runs on).
  *  - Streams: `stream` is a hipStream_t (NULL = the default stream).
  *  - Element strides: (batch, seq, head) strides in elements; the head_dim axis must be contiguous; input base
  *    pointers 16-byte aligned and strides multiples of 8 elements (the quantizers load 16-byte vectors).
@@ -201,6 +202,22 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
                         float qs_mul, const void* mask, int mask_dtype, int64_t msb, int64_t msh, int64_t msq,
                         int8_t* q8, float* qs, int8_t* k8, float* ks, uint8_t* v8t, float* vs, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/*
+ * sage_forward without any allocation: the intermediates (Q8, QS, K8, KS, V8T, VS) and the workspace live in the
+ * library's own device array of SAGE_NOALLOC_SCRATCH_BYTES per GPU (each GPU the library runs on holds its copy until
+ * the process ends); the caller passes only the inputs and the output, with sage_forward's meaning.  For callers
+ * that cannot call hipMalloc or an allocating library (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it).  No counterpart in the reference.  A shape whose intermediates and workspace exceed the array
+ * returns SAGE_ERR_INVALID (128 MiB holds e.g. [1, 24, 4608, 128], 69 MB, and [2, 32/8, 8192, 128], 103 MB).  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU (different streams or threads without
+ * ordering) race; calls ordered on one stream do not.  Nothing in the array needs clearing between calls.
+ */
+#define SAGE_NOALLOC_SCRATCH_BYTES (128ll << 20)
+int sage_forward_noalloc(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb,
+                         int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out,
+                         int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype,
+                         int causal, float qs_mul, void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsage_capi.so"
 
 SAGE_OK, SAGE_ERR_INVALID, SAGE_ERR_UNSUPPORTED, SAGE_ERR_HIP = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F16, DTYPE_BOOL = 0, 1, 2
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 _lock = threading.Lock()
@@ -51,6 +51,8 @@ SIGNATURES = {
     "sage_forward_masked": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
                              _I, _I, _I, _I, _I, _I, _I, _I, _F, _P, _I, _L, _L, _L,
                              _P, _P, _P, _P, _P, _P, _P, _L, _P], _I),
+    "sage_forward_noalloc": ([_P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _L, _L,
+                              _I, _I, _I, _I, _I, _I, _I, _I, _F, _P], _I),
 }
 
 

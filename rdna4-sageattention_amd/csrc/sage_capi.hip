@@ -1,6 +1,9 @@
-// C ABI glue: error reporting, queries and the one-call forward (quantizers -> attention).
+// C ABI glue: error reporting, queries, the one-call forward (quantizers -> attention) and its allocation-free
+// variant on the library's own device scratch array.
 #include <stdio.h>
 #include <string.h>
+
+#include <mutex>
 
 #include "sage_host.h"
 
@@ -45,11 +48,41 @@ static int forward_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int 
   return SAGE_OK;
 }
 
+// ---- scratch of sage_forward_noalloc ----------------------------------------------------------------------------
+// Device memory for the intermediates and workspace of sage_forward_noalloc, for callers that cannot allocate.  Each
+// GPU the library runs on holds its own copy until the process ends.  In host code `scratch` is only a stand-in for
+// the symbol: its device address, different on every GPU, comes from hipGetSymbolAddress (scratch_base) and only that
+// address is ever handed to kernels.
+static __device__ __align__(256) uint8_t scratch[SAGE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static void* g_scratch[MAX_DEVICES] = {};
+static std::mutex g_scratch_mu;
+
+// The current device's address of `scratch`, looked up once per device with that device current.
+static int scratch_base(void** base) {
+  int dev = 0;
+  SAGE_HIP_CHECK(hipGetDevice(&dev), "hipGetDevice");
+  SAGE_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "sage_forward_noalloc: device %d beyond the %d the library tracks", dev,
+               MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    SAGE_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    SAGE_REQUIRE(ptr != nullptr && ((uintptr_t)ptr & 255u) == 0, "sage_forward_noalloc: scratch address %p", ptr);
+    g_scratch[dev] = ptr;
+  }
+  *base = g_scratch[dev];
+  return SAGE_OK;
+}
+
+static int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
 }  // namespace sage
 
 extern "C" {
 
-int sage_abi_version(void) { return 5; }
+int sage_abi_version(void) { return 6; }
 
 const char* sage_last_error(void) { return sage::g_err; }
 
@@ -117,6 +150,43 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
     return rc;
   return sage::attn_impl(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype, nullptr,
                          attn_bytes ? workspace : nullptr, attn_bytes, stream);
+}
+
+int sage_forward_noalloc(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb,
+                         int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, void* out,
+                         int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype,
+                         int causal, float qs_mul, void* stream) {
+  sage::clear_error();
+  const char* who = "sage_forward_noalloc";
+  SAGE_REQUIRE(B > 0 && H > 0 && Hkv > 0 && Sq > 0 && Skv > 0, "%s: sizes must be positive", who);
+  SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
+  if (!sage::head_dim_ok(D)) return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 96, 128, 256)", who, D);
+  if (causal && Sq > Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len <= kv_len", who);
+  // the intermediates of sage_forward, then its workspace, each 256-byte aligned
+  const int64_t dl = sage::layout_dim(D), skp = sage::kv_pad(Skv);
+  const int64_t nq = (int64_t)B * H * Sq, nkv = (int64_t)B * Hkv;
+  int64_t attn_bytes = 0, ws_bytes = 0;
+  int rc = sage::forward_workspace(B, H, Hkv, Sq, Skv, D, causal, &attn_bytes, &ws_bytes);
+  if (rc) return rc;
+  const int64_t o_q8 = 0;
+  const int64_t o_qs = o_q8 + sage::align256(nq * dl);
+  const int64_t o_k8 = o_qs + sage::align256(nq * 4);
+  const int64_t o_ks = o_k8 + sage::align256(nkv * skp * dl);
+  const int64_t o_v8t = o_ks + sage::align256(nkv * (skp / SAGE_KV_BLOCK) * 4);
+  const int64_t o_vs = o_v8t + sage::align256(nkv * dl * skp);
+  const int64_t o_ws = o_vs + sage::align256(nkv * dl * 4);
+  const int64_t need = o_ws + ws_bytes;
+  if (need > (int64_t)SAGE_NOALLOC_SCRATCH_BYTES)
+    return sage::fail(SAGE_ERR_INVALID, "%s: this shape needs %lld bytes of scratch, the library holds %lld "
+                      "(use sage_forward with caller-owned buffers)", who, (long long)need,
+                      (long long)SAGE_NOALLOC_SCRATCH_BYTES);
+  void* base = nullptr;
+  if ((rc = sage::scratch_base(&base))) return rc;
+  uint8_t* p = static_cast<uint8_t*>(base);
+  return sage_forward(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D,
+                      dtype, causal, qs_mul, reinterpret_cast<int8_t*>(p + o_q8), reinterpret_cast<float*>(p + o_qs),
+                      reinterpret_cast<int8_t*>(p + o_k8), reinterpret_cast<float*>(p + o_ks), p + o_v8t,
+                      reinterpret_cast<float*>(p + o_vs), p + o_ws, ws_bytes, stream);
 }
 
 }  // extern "C"

@@ -187,3 +187,18 @@ def test_masked_forward_validates_before_launching():
     assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 80, 0, B, 0, 0, 0, ctypes.byref(ws)) == _capi.SAGE_ERR_UNSUPPORTED
     assert lib.sage_mask_workspace(1, 4, 2, 80, 200, 128, 0, B, 0, 0, 0, None) == _capi.SAGE_ERR_INVALID
     assert ws.value == -1
+
+
+def test_forward_noalloc_rejects_before_touching_the_gpu():
+    """sage_forward_noalloc validates shapes like sage_forward and refuses a shape whose intermediates and workspace
+    exceed its static scratch array (causal shapes plan without querying the device, so this runs without a GPU)."""
+    lib = _capi.lib()
+    args = (P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128)
+    rc = lib.sage_forward_noalloc(*args, 1, 4, 2, 80, 64, 128, 0, 1, 1.0, None)
+    assert rc == _capi.SAGE_ERR_UNSUPPORTED and "causal" in _err()
+    rc = lib.sage_forward_noalloc(*args, 1, 4, 2, 64, 64, 80, 0, 0, 1.0, None)
+    assert rc == _capi.SAGE_ERR_UNSUPPORTED and "head_dim 80" in _err()
+    rc = lib.sage_forward_noalloc(*args, 1, 40, 40, 32760, 32760, 128, 0, 1, 1.0, None)
+    assert rc == _capi.SAGE_ERR_INVALID and "scratch" in _err() and str(128 << 20) in _err()
+    # the array's own size: 128 MiB, the value the header states
+    assert "(128ll << 20)" in HEADER.read_text()
