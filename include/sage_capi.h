@@ -3,7 +3,7 @@
  *
  * This library replaces the reference's native launch boundary: rdna4_sage loads ahead-of-time code objects and
  * launches them with hipModuleLaunchKernel and a packed kernarg block per manifest entry
- * (src/rdna4_sage/_hip.py:52-73, kernel_build/build_kernels.py:330-333).  Here each of those launches is a typed C
+ * (src/rdna4_sage/_hip.py:52-73, kernel_build/build_kernels.py:34-37).  Here each of those launches is a typed C
  * entry point that takes plain device pointers, sizes and element strides, validates them on the host and launches
  * hipcc-built gfx950 kernels on the caller's stream.  Arguments are passed by value (no shared packing buffer), so
  * entry points are reentrant; nothing synchronises.
@@ -53,7 +53,7 @@ extern "C" {
 #define SAGE_DTYPE_F16 1
 #define SAGE_DTYPE_BOOL 2 /* attention masks only */
 
-#define SAGE_KV_BLOCK 32  /* keys per K scale (kernel_build/build_kernels.py:326) */
+#define SAGE_KV_BLOCK 32  /* keys per K scale (kernel_build/build_kernels.py:30) */
 #define SAGE_KV_PAD 128   /* K8 / V8T rows are padded to a multiple of this */
 
 /* ABI version of this header (bumped on any signature change). */
@@ -74,8 +74,8 @@ const char* sage_manifest_json(void);
 
 /*
  * Hadamard-rotate Q over head_dim and quantize to int8 with one scale per token.
- * Replaces the quant_q launch of src/rdna4_sage/_attention.py:125-126 (kernel kernel_build/sage_quant.py:246-261,
- * kernarg "<4Q5i4x2Q", build_kernels.py:332) and folds the sm_scale multiply of _attention.py:130-131:
+ * Replaces the quant_q launch of src/rdna4_sage/_attention.py:125-126 (kernel kernel_build/sage_quant.py:33-48,
+ * kernarg "<4Q5i4x2Q", build_kernels.py:36) and folds the sm_scale multiply of _attention.py:130-131:
  * QS = fp32(fp32(s / D) * qs_mul); pass qs_mul = 1.0f for the default scale.
  * q: [B, Sq, H, D] addressed as q + b*sb + s*ss + h*sh.
  */
@@ -93,7 +93,7 @@ int sage_v_amax(const void* v, int64_t sb, int64_t ss, int64_t sh, int B, int Hk
 /*
  * Hadamard-rotate K and quantize to int8 (one scale per 32 keys); quantize V to E4M3 with the per-channel scale
  * 448 / max(vs, 1e-30) and store it transposed.  Replaces the quant_kv launch of src/rdna4_sage/_attention.py:127-129
- * (kernel kernel_build/sage_quant.py:264-283, kernarg "<7Q9i4x2Q", build_kernels.py:333).
+ * (kernel kernel_build/sage_quant.py:51-70, kernarg "<7Q9i4x2Q", build_kernels.py:37).
  */
 int sage_quant_kv(const void* k, int64_t ksb, int64_t kss, int64_t ksh, const void* v, int64_t vsb, int64_t vss,
                   int64_t vsh, int B, int Hkv, int Skv, int D, int dtype, const float* vs, int8_t* k8, float* ks,
@@ -112,7 +112,7 @@ int sage_attn_plan(int B, int H, int Sq, int Skv, int D, int causal, int* n_full
  * int8 QK^T / fp8 PV flash attention with the reference's online softmax (lazy rescale, threshold 8 in log2
  * units), causal (bottom-right aligned: query i sees keys j <= i + Skv - Sq; requires Sq <= Skv) and grouped-query
  * heads (H % Hkv == 0).
- * Replaces the attn launch of src/rdna4_sage/_attention.py:133-139 (kernarg "<4Q3i4x6Q2i", build_kernels.py:331).
+ * Replaces the attn launch of src/rdna4_sage/_attention.py:133-139 (kernarg "<4Q3i4x6Q2i", build_kernels.py:35).
  * out: out + b*osb + s*oss + h*osh (element strides, head_dim contiguous), dtype out_dtype.
  * lse: optional fp32 [B, H, Sq] (natural-log logsumexp of the quantized logits); pass NULL to skip.
  * workspace: NULL, or at least the sage_attn_plan bytes for this shape (see "Workspace" above).
@@ -126,7 +126,7 @@ int sage_attn_fwd(const int8_t* q8, const float* qs, const int8_t* k8, const flo
  * Row logsumexp of (Q K^T) * sm_scale over the keys (natural log), fp32 [B, H, Sq], computed from the bf16 / fp16
  * inputs with 16-bit MFMAs and fp32 accumulation (the value `return_lse` returns).  sm_scale <= 0 means 1/sqrt(D).
  * Causal masks are bottom-right aligned and need Sq <= Skv.  q / k addressed like sage_quant_q / sage_quant_kv.
- * Replaces the fp32 torch matmul + logsumexp of src/sageattention/core.py:36-57 (`_lse`).
+ * Replaces the fp32 torch matmul + logsumexp of src/sageattention/core.py:23-44 (`_lse`).
  */
 int sage_lse_fwd(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
                  int64_t ksh, int B, int H, int Hkv, int Sq, int Skv, int D, int dtype, int causal, float sm_scale,

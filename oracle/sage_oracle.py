@@ -7,8 +7,8 @@ TEST INFRASTRUCTURE ONLY.  This module is the checker for the gfx950 HIP path: o
 What each function restates (paths relative to the reference checkout):
 
 * ``hadamard_pm1``      src/rdna4_sage/_attention.py:48-56 (Sylvester +-1 matrix, order RB = head_dim for
-                        head_dim 64 / 128, kernel_build/build_kernels.py:336-337, :398-400).
-* ``fwht_rows``         the rotation x = row @ Hm of kernel_build/sage_quant.py:225-243 (`_load_qk`).  The
+                        head_dim 64 / 128, kernel_build/build_kernels.py:40-41, :102-104).
+* ``fwht_rows``         the rotation x = row @ Hm of kernel_build/sage_quant.py:12-30 (`_load_qk`).  The
                         reference accumulates the +-1 products in fp32 inside ``tl.dot`` in an order that the
                         gfx12 hardware fixes and that is not recoverable here.  This build defines the rotation
                         as a float64 fast Walsh-Hadamard transform in a fixed stage order (stage bit 0 first,
@@ -17,21 +17,25 @@ What each function restates (paths relative to the reference checkout):
                         magnitude, so the result is the correctly rounded fp32 of the exact sum; it equals the
                         reference's fp32 accumulation whenever that accumulation is exact.  The HIP kernels run
                         the same stages in the same order, so the two agree bit for bit in every case.
-* ``quant_q``           kernel_build/sage_quant.py:246-261 (`_quant_q`) plus the sm_scale fold of
+* ``quant_q``           kernel_build/sage_quant.py:33-48 (`_quant_q`) plus the sm_scale fold of
                         src/rdna4_sage/_attention.py:130-131.
 * ``v_amax``            src/rdna4_sage/_attention.py:120-121 (`vector_norm(v, inf, dim=seq, dtype=fp32)`).
-* ``quant_kv``          kernel_build/sage_quant.py:264-283 (`_quant_kv`).
-* ``f32_to_e4m3``       the fp32 -> float8 E4M3FN cast of sage_quant.py:283 (round to nearest even, subnormals
+* ``quant_kv``          kernel_build/sage_quant.py:51-70 (`_quant_kv`).
+* ``f32_to_e4m3``       the fp32 -> float8 E4M3FN cast of sage_quant.py:70 (round to nearest even, subnormals
                         kept; inputs are clamped to +-448 first so the NaN code is never produced).
 * ``attention``         the FlyDSL kernel's math as rewritten by kernel_build/make_sage.py:75-107, :196-237,
                         make_sage_r2.py:54-269 and make_sage_pkg.py:74-87: int32 S = Q8 K8^T, per-32-key K scale,
                         lazy rescale with threshold 8.0 (log2 units), exp2, P cast to E4M3, fp32 PV
-                        accumulation, epilogue (O * ((1/448) / l)) * VS.  ``block_n`` is the KV tile of the
-                        online softmax: 32 in the reference (kernel_build/compile_attn.py:109), 64 in this
-                        build's gfx950 kernel.  The exponent argument is the gfx950 kernel's
+                        accumulation, epilogue (O * ((1/448) / l)) * VS.  ``block_n`` is the key block of the
+                        online softmax, one lazy-rescale decision each: 32 in the reference
+                        (kernel_build/compile_attn.py:19); the gfx950 kernel walks 64-key tiles but decides per
+                        32-key block as well, so the GPU tests compare at 32 (64 serves the oracle's own
+                        identities).  Split key ranges and additive-mask classes follow the kernel's 64-key tiles
+                        whatever block_n.  For head dims up to 128 the exponent argument is the gfx950 kernel's
                         fma(c + S * 2^-26, ct * 2^26, nk) form (c = fp32(1 / (2 pi))), which differs from the
                         reference's S * ct - cl * m by the rounding of nk (at most 1.5 * ct: S moved by less than
-                        2 units, far below the int8 quantization error of S and the E4M3 step of p).
+                        2 units, far below the int8 quantization error of S and the E4M3 step of p); head dim 256
+                        uses fma(fp32(S), ct, -cl * m), the reference's own form.
                         Bottom-right causal for any q_len / kv_len: query i sees keys j <= i + kv_len - q_len; a
                         query that sees no key (q_len > kv_len) gives a 0 row (the gfx950 convention; the reference
                         sends such calls to SDPA, so this case has no reference value).
@@ -45,7 +49,7 @@ What each function restates (paths relative to the reference checkout):
                         (softmax shift invariance) identities and by float64 attention with the same bias.
 * ``sage_forward_varlen`` src/sageattention/core.py:66-89 (`sageattn_varlen`): one ``sage_forward`` per sequence
                         of the packed batch.
-* ``lse_reference``     src/sageattention/core.py:36-57 (`_lse`).
+* ``lse_reference``     src/sageattention/core.py:23-44 (`_lse`).
 
 All float32 steps are written as float32 numpy operations, which round to nearest even like the GPU's
 float32 ALU.  ``exp2`` and the order of the fp32 additions inside the PV product are implementation-defined
@@ -59,7 +63,7 @@ import math
 import numpy as np
 
 F32 = np.float32
-KV_BLOCK = 32          # one K scale per 32 keys (kernel_build/build_kernels.py:326)
+KV_BLOCK = 32          # one K scale per 32 keys (kernel_build/build_kernels.py:30)
 E4M3_MAX = 448.0
 RESCALE_THRESHOLD = 8.0  # make_sage.py:219-225: keep a stale max until it is exceeded by 2^8
 LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
@@ -152,7 +156,7 @@ def rotate_rows(x: np.ndarray) -> np.ndarray:
 # Rounding helpers
 # ----------------------------------------------------------------------------------------------------------
 def round_half_away_i8(y: np.ndarray) -> np.ndarray:
-    """int8(trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)))  (sage_quant.py:257, :278)."""
+    """int8(trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)))  (sage_quant.py:44, :65)."""
     y = y.astype(F32)
     t = np.where(y >= 0, y + F32(0.5), y - F32(0.5)).astype(F32)
     return np.trunc(t).astype(np.int8)
@@ -202,7 +206,7 @@ def qs_fold_factor(sm_scale, d: int):
 def quant_q(q: np.ndarray, sm_scale=None):
     """q: [B, H, S, D] float32 holding bf16/fp16 values (HND).
 
-    Returns (q8 int8 [B, H, S, D], qs float32 [B, H, S]).  sage_quant.py:246-261; scale / RB because the
+    Returns (q8 int8 [B, H, S, D], qs float32 [B, H, S]).  sage_quant.py:33-48; scale / RB because the
     unnormalised Hadamard multiplies Q K^T by RB (:259-260), the scale itself without rotation (d = 96); optional
     sm_scale fold (_attention.py:130-131)."""
     d = q.shape[-1]
@@ -234,7 +238,7 @@ def quant_kv(k: np.ndarray, v: np.ndarray, vs: np.ndarray | None = None, seq_pad
     """k, v: [B, Hkv, S, D] float32 holding bf16/fp16 values.
 
     Returns (k8 int8 [B, Hkv, Sp, D], ks float32 [B, Hkv, Sp/32], v8 uint8 E4M3 bits [B, Hkv, Sp, D],
-    vs float32 [B, Hkv, D]) in natural key order; rows >= S are zero.  sage_quant.py:264-283."""
+    vs float32 [B, Hkv, D]) in natural key order; rows >= S are zero.  sage_quant.py:51-70."""
     B, Hkv, S, D = k.shape
     sp = padded_len(S, KV_BLOCK) if seq_pad is None else seq_pad
     assert sp % KV_BLOCK == 0 and sp >= S
@@ -572,7 +576,7 @@ def sdpa_reference(q, k, v, causal=False, sm_scale=None, attn_mask=None):
 
 
 def lse_reference(q, k, causal=False, sm_scale=None):
-    """logsumexp_j(q_i . k_j * scale) in float64 (src/sageattention/core.py:36-57), [B, H, Sq]."""
+    """logsumexp_j(q_i . k_j * scale) in float64 (src/sageattention/core.py:23-44), [B, H, Sq]."""
     B, H, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
     kk = np.repeat(k.astype(np.float64), H // Hkv, axis=1)

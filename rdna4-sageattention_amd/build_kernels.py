@@ -1,6 +1,6 @@
 """Ahead-of-time build of the gfx950 kernels: hipcc -> cdna4_sage/libsage_capi.so (+ cdna4_sage/manifest.json).
 
-Replaces the reference's offline kernel build (kernel_build/build_kernels.py:413-438, which ran FlyDSL and Triton
+Replaces the reference's offline kernel build (kernel_build/build_kernels.py:117-142, which ran FlyDSL and Triton
 and wrote one code object per variant plus kernels/manifest.json).  Here every variant (layouts of 64 / 128 / 256
 channels for head dims 64, 96, 128, 256 x bf16/f16 x causal/non-causal x dense/varlen) is compiled by hipcc into one
 shared library; the manifest is the library's own description

@@ -200,7 +200,7 @@ def _out_strides(out: torch.Tensor):
 
 def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
     """Row logsumexp of Q K^T * scale (natural log) over the keys, fp32 [B, H, q_len], from the 16-bit inputs on the
-    gfx950 LSE kernel (the value `return_lse` returns; reference: src/sageattention/core.py:36-57).  Causal masks are
+    gfx950 LSE kernel (the value `return_lse` returns; reference: src/sageattention/core.py:23-44).  Causal masks are
     bottom-right aligned and need q_len <= kv_len.  Raises Unsupported when the kernel cannot run these inputs."""
     if layout not in ("HND", "NHD"):
         raise Unsupported(f"layout {layout!r}")
@@ -223,7 +223,7 @@ def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
     if is_causal and Sq > Skv:
         raise Unsupported("causal LSE needs q_len <= kv_len")
     if sm_scale is not None and not sm_scale > 0:
-        # the reference's _lse takes an explicit scale as given (src/sageattention/core.py:30); the kernel's 0 means
+        # the reference's _lse takes an explicit scale as given (src/sageattention/core.py:31); the kernel's 0 means
         # the default 1 / sqrt(head_dim), so such scales go to the torch formula
         raise Unsupported("sm_scale <= 0")
     q, sq_ = _bsh(q, layout)

@@ -1,10 +1,10 @@
 """ctypes binding of libsage_capi.so (the C ABI declared in include/sage_capi.h).
 
-Replaces the reference's driver-API FFI (src/rdna4_sage/_hip.py:141-213): instead of packing kernarg blocks into a
+Replaces the reference's driver-API FFI (src/rdna4_sage/_hip.py:1-73): instead of packing kernarg blocks into a
 shared ctypes buffer per kernel and calling hipModuleLaunchKernel, each launch is a typed C call with arguments
 passed by value, so concurrent callers cannot clobber each other's arguments.  torch is imported before the library
 is opened, so the library binds to the HIP runtime instance torch already loaded (same soname) and shares its device
-context and streams, which is the reason the reference looks the runtime up in /proc/self/maps (_hip.py:151-168).
+context and streams, which is the reason the reference looks the runtime up in /proc/self/maps (_hip.py:11-28).
 """
 from __future__ import annotations
 

@@ -1,7 +1,7 @@
 // int8 QK^T / fp8 PV flash attention for gfx950 (CDNA4, wave64 MFMA).
 //
 // Math (the reference kernel's: kernel_build/make_sage.py:75-107, :196-237; make_sage_r2.py:52-269, 32-key tiles
-// per kernel_build/compile_attn.py:20):
+// per kernel_build/compile_attn.py:19):
 //   cl_i   = fp32(sm * log2e) * QS_i                      (sm = 1/sqrt(D) baked in; other scales folded into QS)
 //   S_ij   = sum_d Q8_id K8_jd                            (int32, exact; |S| <= 127^2 * D)
 //   per 32-key block (one K scale KS_block each, make_sage_r2.py:141-190):

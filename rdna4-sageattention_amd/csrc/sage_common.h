@@ -7,7 +7,7 @@
 //  * x / s with s shared by a whole row or block: r = RN(1 / s) once, then y0 = x * r, e = fma(-y0, s, x),
 //    y = fma(e, r, y0), which equals the IEEE quotient RN(x / s) (Markstein's correction with a correctly rounded
 //    reciprocal; the remainder e is exact because y0 is within one ulp of x / s).
-//  * int8 rounding: trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)) (kernel_build/sage_quant.py:257, :278).
+//  * int8 rounding: trunc(y >= 0 ? fp32(y + 0.5) : fp32(y - 0.5)) (kernel_build/sage_quant.py:44, :65).
 //  * fp32 -> E4M3FN: round to nearest even with subnormals, inputs already clamped to +-448.
 // Every translation unit is compiled with -ffp-contract=off: the only fused multiply-adds are the explicit ones.
 #pragma once

@@ -1,5 +1,5 @@
 // Row logsumexp of (Q K^T) * sm_scale over the keys, natural log, fp32 [B, H, Sq], on the bf16 / fp16 inputs
-// (what `return_lse` returns; reference: src/sageattention/core.py:36-57, an fp32 torch matmul plus logsumexp per row
+// (what `return_lse` returns; reference: src/sageattention/core.py:23-44, an fp32 torch matmul plus logsumexp per row
 // chunk).  Products of two 16-bit floats are exact in fp32, so the MFMA's fp32 accumulation gives the scores to fp32
 // accuracy, as the reference's fp32 matmul does.
 //

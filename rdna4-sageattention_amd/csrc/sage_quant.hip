@@ -1,11 +1,11 @@
 // Quantization kernels of the gfx950 SageAttention path (HBM-bound streaming kernels).
 //
-//  quant_q_kernel   Q rows -> Hadamard (float64 FWHT) -> int8, one scale per token   (sage_quant.py:246-261)
+//  quant_q_kernel   Q rows -> Hadamard (float64 FWHT) -> int8, one scale per token   (sage_quant.py:33-48)
 //  fill_kernel      clears the V amax buffer (a kernel, not hipMemsetAsync, so the sequence can be graph-captured)
 //  v_amax_kernel    per-channel max |v| over a chunk of rows, combined with atomicMax on the fp32 bit pattern
 //                   (values are >= 0, so unsigned order == float order)               (_attention.py:120-121)
 //  quant_kv_kernel  K rows -> Hadamard -> int8, one scale per 32 keys; V -> E4M3 with the per-channel scale,
-//                   transposed through LDS into V8T                                  (sage_quant.py:264-283)
+//                   transposed through LDS into V8T                                  (sage_quant.py:51-70)
 //  quant_qk_vamax_kernel, quant_v_kernel   the same work in sage_forward's two launches
 //  quant_varlen_kernel, quant_v_varlen_kernel   packed variable-length batches
 //
@@ -104,7 +104,7 @@ __device__ __forceinline__ void quant_q_rows(const uint16_t* __restrict__ x, int
   const float r = 1.0f / s;
   int8_t* dst = q8 + ((int64_t)bh * S + row) * HD::DP + j * EPL;
   quantize_store_i8<EPL>(xf, s, r, dst, valid);
-  // the unnormalised rotation multiplies Q K^T by RB (sage_quant.py:259-260); no rotation, no division
+  // the unnormalised rotation multiplies Q K^T by RB (sage_quant.py:46-47); no rotation, no division
   if (valid && j == 0) qs[(int64_t)bh * S + row] = (HD::ROT ? s / (float)HD::RB : s) * qs_mul;
 }
 

@@ -1,6 +1,6 @@
 """SageAttention 2.2 API on top of cdna4_sage (AMD MI355X, gfx950).
 
-Every public function of SageAttention 2.2 keeps its signature (reference: src/sageattention/core.py:60-142).  All of
+Every public function of SageAttention 2.2 keeps its signature (reference: src/sageattention/core.py:47-129).  All of
 them run the same path (Hadamard-rotated int8 Q K^T, fp8 P V with per-channel V scales); kernel-selection arguments
 such as qk_quant_gran, pv_accum_dtype, smooth_k, smooth_v or value_dtype are accepted and ignored.  Calls the gfx950
 kernels cannot run or would not win on (small problems, unsupported head dims or GPUs, masks of another dtype) use torch
@@ -26,7 +26,7 @@ def _as_hnd(t: torch.Tensor, tensor_layout: str) -> torch.Tensor:
 
 def _lse(q, k, tensor_layout, is_causal, sm_scale):
     """Row logsumexp of Q K^T * scale over the keys, fp32 [B, H, q_len], on the unquantized inputs
-    (reference: src/sageattention/core.py:36-57).  Causal masks are bottom-right aligned.  On gfx950 the LSE kernel
+    (reference: src/sageattention/core.py:23-44).  Causal masks are bottom-right aligned.  On gfx950 the LSE kernel
     computes it (16-bit products exact in fp32, fp32 accumulation); elsewhere, and for shapes the kernel does not take,
     the query heads that share a kv head are processed together with one fp32 batched product per row chunk."""
     _as_hnd(q, tensor_layout)  # layout check (ValueError, as the reference)

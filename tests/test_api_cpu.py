@@ -128,8 +128,8 @@ def test_fake_impl_shapes():
 @pytest.mark.parametrize("layout", ["HND", "NHD"])
 @pytest.mark.parametrize("causal", [False, True])
 def test_return_lse_matches_float64(layout, causal):
-    """LSE semantics of src/sageattention/core.py:36-57 (unquantized fp32, bottom-right causal, GQA) against a
-    float64 logsumexp; the reference's gate is atol 2e-3, rtol 1e-4 (tests/test_sageattention.py:77)."""
+    """LSE semantics of src/sageattention/core.py:23-44 (unquantized fp32, bottom-right causal, GQA) against a
+    float64 logsumexp; the reference's gate is atol 2e-3, rtol 1e-4 (tests/test_sageattention.py:70)."""
     q = _rand((1, 4, 70, 64), 11, torch.float16)
     k, v = _rand((1, 2, 90, 64), 12, torch.float16), _rand((1, 2, 90, 64), 13, torch.float16)
     if layout == "NHD":
@@ -280,7 +280,7 @@ def test_autograd_inputs_reach_the_registered_op(monkeypatch):
 
 
 def test_lse_with_non_positive_sm_scale_uses_it_as_given():
-    """The reference's _lse multiplies by an explicit sm_scale as given (src/sageattention/core.py:30), 0 and negative
+    """The reference's _lse multiplies by an explicit sm_scale as given (src/sageattention/core.py:31), 0 and negative
     values included; the LSE kernel entry leaves such scales to the torch formula."""
     q = _rand((1, 2, 20, 64), 31)
     k = _rand((1, 2, 40, 64), 32)

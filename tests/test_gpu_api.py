@@ -17,7 +17,7 @@ import sageattention
 
 pytestmark = pytest.mark.gpu
 
-COS = 0.998   # the reference's gate (tests/test_attention.py:175, tests/test_sageattention.py:14)
+COS = 0.998   # the reference's gate (tests/test_attention.py:54, tests/test_sageattention.py:14)
 
 
 def ref_attention(q, k, v, layout="HND", causal=False, scale=None, heads=None):

@@ -1,7 +1,7 @@
 """gfx950 attention kernel vs the CPU emulation of the reference's quantized math and vs float attention.
 
 Tolerances (north star): max |out - emulation| <= 2e-2 with the emulation taking the reference's lazy-rescale
-decisions once per 32-key block (kernel_build/compile_attn.py:20), and cosine >= 0.999 against float attention; the
+decisions once per 32-key block (kernel_build/compile_attn.py:19), and cosine >= 0.999 against float attention; the
 reference's own gate is cosine > 0.998 (tests/test_attention.py:54).  Beyond the north star, the kernel follows the
 emulation element by element: the exp2 implementation and the fp32 summation order inside the PV MFMA are the only
 differences, so most output elements are the emulation's bits and the rest move by a probability whose E4M3 rounding

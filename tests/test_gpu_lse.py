@@ -96,7 +96,7 @@ def test_return_lse_side_stream_joins_the_callers_stream(dev):
 
 
 def test_return_lse_with_non_positive_sm_scale_uses_it_as_given(dev):
-    """An explicit sm_scale <= 0 is taken as given by the reference's _lse (src/sageattention/core.py:30): the LSE
+    """An explicit sm_scale <= 0 is taken as given by the reference's _lse (src/sageattention/core.py:31): the LSE
     kernel entry refuses it and the torch formula computes it, 0 giving log(kv_len)."""
     q, k = _inputs(1, 2, 2, 300, 1100, 128, torch.bfloat16, "HND", seed=9)
     qd, kd = q.to(dev), k.to(dev)

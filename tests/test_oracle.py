@@ -76,7 +76,7 @@ def test_fwht_float32_is_correctly_rounded_exact_sum(dtype):
 
 # ------------------------------------------------------------------------------------------------ rounding helpers
 def test_round_half_away_matches_exact_definition():
-    """int8 conversion = trunc(RN32(y +- 0.5)) (reference: sage_quant.py:257): ties go away from zero and values
+    """int8 conversion = trunc(RN32(y +- 0.5)) (reference: sage_quant.py:44): ties go away from zero and values
     just below a half can still round up through the fp32 addition."""
     ys = [0.5, -0.5, 1.5, -1.5, 2.5, 126.5, -126.5, 0.49999997, -0.49999997, 0.0, -0.0, 127.0, -127.0, 3.4999998]
     ys += list(np.random.default_rng(2).uniform(-127.4, 127.4, 2000).astype(F32))
@@ -211,7 +211,7 @@ def test_quant_kv_invariants_and_vector_norm():
     blk = np.abs(k8.astype(int)).reshape(1, 2, 4, 32, 64).max(axis=(-1, -2))
     assert np.all(blk == 127)                                         # each 32-key block spans the int8 range
     x = orc.fwht_rows(k).astype(F32)
-    # KS is max|x| / 127 of the block and is NOT divided by the rotation order (sage_quant.py:276-279)
+    # KS is max|x| / 127 of the block and is NOT divided by the rotation order (sage_quant.py:63-66)
     assert np.allclose(ks[:, :, 0] * 127, np.abs(x[:, :, :32]).max(axis=(-1, -2)), rtol=1e-6)
     dec = orc.e4m3_to_f32(v8[:, :, :100])
     assert np.all(dec[..., 5] == 0)                                   # zero channel stays zero
