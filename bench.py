@@ -11,9 +11,12 @@ Prints ONE JSON line on stdout:
   cpu_baseline the reference's quantized math (the numpy port in oracle/) timed on this host on a head sample
 Everything else (per-kernel times, quantizer GB/s, torch SDPA bf16 on the same GPU) goes to the "detail" object.
 
-usage: python bench.py [--gpus 1] [--steps 100] [--warmup W] [--no-cpu-baseline] [--config 2]
-(default W: at least 20 steps and 0.3 s, enough for the GPU clock to leave its idle state: the first ~25 ms of calls
-run ~15% slower)
+usage: python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--no-cpu-baseline] [--config 2]
+
+Order: 0.3 s of forward calls take the GPU clock out of its idle state (in which the first ~25 ms of calls run ~15%
+slower), then the per-kernel, SDPA and masked-call measurements run, then exactly --warmup untimed steps and the --steps
+timed ones (mean time per call, back to back).  detail.median_synced_ms adds the reference's method
+(tests/bench_models.py:45-53: 3 warm-up calls, then the median of 10 calls each followed by a synchronisation).
 """
 from __future__ import annotations
 
@@ -21,6 +24,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -117,9 +121,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=None,
-                    help="untimed steps before the timed ones (default: at least 20 and at least 0.3 s of steps, so "
-                         "that the GPU clock has left its idle state)")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed steps right before the timed ones")
     ap.add_argument("--config", default="2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=50)
@@ -163,23 +165,7 @@ def main():
         # below the router's minimum size sageattn uses SDPA, as the reference does: time the kernel-forced entry
         def step():
             return cdna4_sage.attention(q, k, v, "HND", is_causal=cfg.causal)
-    if args.warmup is None:
-        step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        step()
-        torch.cuda.synchronize()
-        args.warmup = max(20, math.ceil(0.3 / max(time.perf_counter() - t0, 1e-6)))
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ops = cfg.attention_ops()
-    tops = ops / (ms * 1e-3) / 1e12
 
     # ---- per-kernel times: the same launches the call makes, each looped on torch's current stream ----
     B, H, Hkv, S, D = cfg.B, cfg.H, cfg.Hkv, cfg.S, cfg.D
@@ -218,8 +204,12 @@ def main():
                         int(cfg.causal), dt, None, ws.data_ptr() if split and ws_bytes else None,
                         ws_bytes if split else 0, st)
 
-    k_forward()
-    torch.cuda.synchronize()
+    # the GPU clock leaves its idle state within ~25 ms of busy calls: spin the forward for 0.3 s before any timing
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.3:
+        for _ in range(10):
+            k_forward()
+        torch.cuda.synchronize()
     it = args.kernel_iters
     t_fwd = time_events(k_forward, it)
     t_attn = time_events(k_attn, it)
@@ -229,7 +219,7 @@ def main():
 
     # ---- torch SDPA bf16 on the same GPU, same method as the step ----
     sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=cfg.causal, enable_gqa=Hkv != H)  # noqa: E731
-    for _ in range(args.warmup):
+    for _ in range(20):
         sdpa()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -245,7 +235,7 @@ def main():
         mask = (torch.arange(S, device=dev) < S - S // 8)[None, None, None, :].expand(B, 1, 1, S)
 
         def wall(fn, n):
-            for _ in range(min(args.warmup, 50)):
+            for _ in range(20):
                 fn()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -263,6 +253,28 @@ def main():
                             max(10, args.steps // 10))
         masked = {"mask": f"bool [B, 1, 1, S], first {S - S // 8} of {S} keys visible", "ms": round(ms_mask, 4),
                   "sdpa_bf16_ms": round(ms_mask_sdpa, 4), "speedup_vs_sdpa_bf16": round(ms_mask_sdpa / ms_mask, 3)}
+
+    # ---- the step: exactly --warmup untimed calls, then --steps timed calls back to back ----
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    tops = ops / (ms * 1e-3) / 1e12
+    # the reference's method (tests/bench_models.py:45-53): 3 warm-ups, median of 10 synchronised calls
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    synced = []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        synced.append((time.perf_counter() - t0) * 1e3)
+    ms_median_synced = statistics.median(synced)
 
     traffic, traffic_src = profiled_traffic(args.config)
     result = {
@@ -291,6 +303,7 @@ def main():
         "detail": {
             "step": "sageattention.sageattn" if routed else "cdna4_sage.attention (sageattn routes this size to SDPA)",
             "call_frac_of_peak": round(tops / MFMA_PEAK_TFLOPS, 4),
+            "median_synced_ms": round(ms_median_synced, 4),
             "kernel_ms": {"forward_capi": round(t_fwd, 5), "attn": round(t_attn, 5),
                           "quant (forward - attn)": round(t_fwd - t_attn, 5)},
             "quant_GBps": round(quant_bytes / ((t_fwd - t_attn) * 1e-3) / 1e9, 1),

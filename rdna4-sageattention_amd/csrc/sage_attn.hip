@@ -294,6 +294,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
   float m = -INFINITY, l = 0.0f;
+  float negm = 0.0f;  // -(cl * m_ref), m_ref = m or 0 while m = -inf: the exponent offset while m stays
   v8i pb = {};  // E4M3 probabilities (B operand of the PV MFMA); each cvt rewrites one half, so no clearing
   v4i bw_none[4] = {};  // the bias argument of the tile bodies without an additive mask (never read)
 
@@ -302,12 +303,16 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   // masked (MW = the lane's mask word of the tile); 3: the additive mask values BW (the lane's 32 16-bit values,
   // input dtype, -inf = masked) added in log2 units, with the row max taken over the biased logits.
   // The rescale decision is taken once per 32-key block, as the reference's 32-key tiles take it
-  // (kernel_build/make_sage_r2.py:180-190): block 0 against m, block 1 against the max m1 that block 0 left.  When no
-  // lane of the wave moves its max at block 1, one K = 64 PV MFMA per channel block adds both blocks (the reference's
-  // two PV steps up to the fp32 summation order).  Otherwise (rare: a row's max rising by 2^8 within a tile) the wave
-  // runs the tile body twice before the tile's barrier: pass 0 adds block 0 alone (block 1's bytes of the B operand
-  // cleared, m = m1), pass 1 (REDO) masks block 0 and adds block 1, whose rescale then comes before its MFMA.  No MFMA
-  // sits in a branch: the compiler loses the accumulators' coalescing around one and spills the whole loop.
+  // (kernel_build/make_sage_r2.py:180-190): block 0 against m, block 1 against the max m1 that block 0 left.  A
+  // wave-uniform test first asks whether any lane's larger block max moves its max at all; almost always none does,
+  // and then m, the exponent offset negm and l's scale stay as they are (no per-block work).  Otherwise the per-block
+  // decisions run.  When no lane moves its max at block 1, one K = 64 PV MFMA per channel block adds both blocks (the
+  // reference's two PV steps up to the fp32 summation order).  When some lane does (rare: a row's max rising by 2^8
+  // inside a tile), the wave runs the tile body twice before the tile's barrier: pass 0 adds block 0 alone (block 1's
+  // exponent offset is -inf, so its probabilities, sum and E4M3 bytes are 0, and m = m1), pass 1 (REDO) masks block 0
+  // and adds block 1, whose rescale then comes before its MFMA.  No MFMA sits in a branch: around one the compiler
+  // loses the accumulators' coalescing and spills the whole loop; the O rescale sits in its own branch after the
+  // exponentials for the same reason.
 #define SAGE_TILE(T, MODE, MW, BW, REDO)                                                                       \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
@@ -347,14 +352,12 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     }                                                                                                      \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
-    bool need0_, need1_;    /* block 0 / block 1 rescales */                                               \
-    float m1_, m2_;         /* the max after block 0 / after block 1 */                                    \
-    float carg0_, carg1_;   /* log2 of the rescale factors of the two blocks */                            \
-    float psum0_ = 0.0f, psum1_ = 0.0f;                                                                    \
+    /* the two 32-key blocks' row maxima: MODE 3 in log2 units of the biased logits t (kept in sf_), else in  \
+       m's units, fp32(max S * ks) (scaled by 2^-26 when seeded: mx - c is exact) */                       \
+    float bm0_, bm1_;                                                                                      \
     if ((MODE) == 3) {                                                                                     \
-      /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))): the biased logit in log2 units (b = -inf for a masked \
-         key gives -inf); the lazy rescale compares a block's max of t with m * cl and keeps m in S * ks      \
-         units (m_new = m_cand * (1 / cl)) */                                                               \
+      /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))) (b = -inf for a masked key gives -inf); the lazy         \
+         rescale compares a block's max of t with m * cl and keeps m in S * ks units (m_new = m_cand / cl) */  \
       const float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;      \
       float tm0_ = -INFINITY, tm1_ = -INFINITY;                                                            \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
@@ -366,29 +369,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           if (kb_) tm1_ = fmaxf(tm1_, sf_[kb_][v_]);                                                       \
           else tm0_ = fmaxf(tm0_, sf_[kb_][v_]);                                                           \
         }                                                                                                  \
-      tm0_ = fmaxf(tm0_, xor32_f32(tm0_));                                                                 \
-      tm1_ = fmaxf(tm1_, xor32_f32(tm1_));                                                                 \
-      const float mc0_ = m * cl;                                                                           \
-      const float mcand0_ = fmaxf(mc0_, tm0_);                                                             \
-      need0_ = (mcand0_ - mc0_) > 8.0f;                                                                    \
-      m1_ = need0_ ? mcand0_ * rcl : m;                                                                    \
-      const float mc1_ = m1_ * cl;                                                                         \
-      const float mcand1_ = fmaxf(mc1_, tm1_);                                                             \
-      need1_ = (mcand1_ - mc1_) > 8.0f;                                                                    \
-      m2_ = need1_ ? mcand1_ * rcl : m1_;                                                                  \
-      const float mref1_ = m1_ == -INFINITY ? 0.0f : m1_;                                                  \
-      const float mref2_ = m2_ == -INFINITY ? 0.0f : m2_;                                                  \
-      carg0_ = (m - mref1_) * cl;                                                                          \
-      carg1_ = (m1_ - mref2_) * cl;                                                                        \
-      const float negl1_ = 0.0f - cl * mref1_, negl2_ = 0.0f - cl * mref2_;                                \
-      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
-        sf_[0][v_] = __builtin_amdgcn_exp2f(sf_[0][v_] + negl1_);                                          \
-        psum0_ += sf_[0][v_];                                                                              \
-      }                                                                                                    \
-      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
-        sf_[1][v_] = __builtin_amdgcn_exp2f(sf_[1][v_] + negl2_);                                          \
-        psum1_ += sf_[1][v_];                                                                              \
-      }                                                                                                    \
+      bm0_ = fmaxf(tm0_, xor32_f32(tm0_));                                                                 \
+      bm1_ = fmaxf(tm1_, xor32_f32(tm1_));                                                                 \
     } else {                                                                                               \
       float mx0_, mx1_;                                                                                    \
       if (SEEDED) {                                                                                        \
@@ -411,59 +393,83 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
         mx0_ = fmaxf(mx0_, xor32_f32(mx0_));                                                               \
         mx1_ = fmaxf(mx1_, xor32_f32(mx1_));                                                               \
       }                                                                                                    \
-      /* the block's row max in m's units: fp32(max S * ks), scaled by 2^-26 when seeded (mx - c is exact) */ \
-      const float rm0_ = SEEDED ? (mx0_ - SEED_F) * ks0_ : mx0_ * ks0_;                                    \
-      const float rm1_ = SEEDED ? (mx1_ - SEED_F) * ks1_ : mx1_ * ks1_;                                    \
-      const float mcand0_ = fmaxf(m, rm0_);                                                                \
-      need0_ = (mcand0_ - m) * cl > 8.0f;                                                                  \
-      m1_ = need0_ ? mcand0_ : m;                                                                          \
-      const float mcand1_ = fmaxf(m1_, rm1_);                                                              \
-      need1_ = (mcand1_ - m1_) * cl > 8.0f;                                                                \
-      m2_ = need1_ ? mcand1_ : m1_;                                                                        \
+      bm0_ = SEEDED ? (mx0_ - SEED_F) * ks0_ : mx0_ * ks0_;                                                \
+      bm1_ = SEEDED ? (mx1_ - SEED_F) * ks1_ : mx1_ * ks1_;                                                \
+    }                                                                                                      \
+    /* Does some lane of the wave move its max at either block?  Subtraction and the product with cl > 0 are  \
+       monotonic, so a larger block max can only raise the test: with the larger of the two below the         \
+       threshold, neither block's decision fires (and an -inf max against m = -inf gives NaN, false, as the   \
+       per-block test does).  Then m stays, and so does the exponent offset negm = -(cl * m_ref). */         \
+    const bool any_ = __ballot((MODE) == 3 ? (fmaxf(bm0_, bm1_) - m * cl) > 8.0f                          \
+                                           : (fmaxf(bm0_, bm1_) - m) * cl > 8.0f) != 0;                   \
+    float nk0_, nk1_;       /* the blocks' exponent offsets (MODE 3: added to t) */                        \
+    float corr_ = 1.0f;     /* the rescale before this pass's MFMA */                                      \
+    bool slow_ = false;     /* some lane moves its max at block 1 in a first pass: block 1 waits for pass 1 */ \
+    bool resc_ = false;     /* some lane rescales O before this pass's MFMA */                             \
+    if (!any_) {                                                                                           \
+      nk0_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct0_ : negm;                                        \
+      nk1_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct1_ : negm;                                        \
+    } else {                                                                                               \
+      /* the reference's decisions, block 0 against m, block 1 against the max m1 block 0 left */          \
+      bool need0_, need1_;                                                                                 \
+      float m1_, m2_;                                                                                      \
+      if ((MODE) == 3) {                                                                                   \
+        const float mc0_ = m * cl;                                                                         \
+        const float mcand0_ = fmaxf(mc0_, bm0_);                                                           \
+        need0_ = (mcand0_ - mc0_) > 8.0f;                                                                  \
+        m1_ = need0_ ? mcand0_ * rcl : m;                                                                  \
+        const float mc1_ = m1_ * cl;                                                                       \
+        const float mcand1_ = fmaxf(mc1_, bm1_);                                                           \
+        need1_ = (mcand1_ - mc1_) > 8.0f;                                                                  \
+        m2_ = need1_ ? mcand1_ * rcl : m1_;                                                                \
+      } else {                                                                                             \
+        const float mcand0_ = fmaxf(m, bm0_);                                                              \
+        need0_ = (mcand0_ - m) * cl > 8.0f;                                                                \
+        m1_ = need0_ ? mcand0_ : m;                                                                        \
+        const float mcand1_ = fmaxf(m1_, bm1_);                                                            \
+        need1_ = (mcand1_ - m1_) * cl > 8.0f;                                                              \
+        m2_ = need1_ ? mcand1_ : m1_;                                                                      \
+      }                                                                                                    \
       /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets  \
          from 0 instead of -inf keep corr and the exponents free of NaN */                                 \
-      const float mref1_ = ((MODE) != 0 && m1_ == -INFINITY) ? 0.0f : m1_;                                \
-      const float mref2_ = ((MODE) != 0 && m2_ == -INFINITY) ? 0.0f : m2_;                                \
-      carg0_ = (m - mref1_) * cl;                                                                          \
-      carg1_ = (m1_ - mref2_) * cl;                                                                        \
-      /* p = exp2(fma(F, ct, nk)), nk = -(cl * m_new) - fp32(c * ct) (seeded) or -(cl * m_new) */           \
+      const float mref1_ = m1_ == -INFINITY ? 0.0f : m1_;                                                  \
+      const float mref2_ = m2_ == -INFINITY ? 0.0f : m2_;                                                  \
+      slow_ = !(REDO) && __ballot(need1_) != 0;                                                            \
+      /* nk = -(cl * m_new) - fp32(c * ct) (seeded), -(cl * m_new) (unseeded, and MODE 3 whose t holds the   \
+         seed term); in a slow first pass block 1's offset is -inf, so its p, sum and E4M3 bytes are 0 */    \
       const float neg1_ = 0.0f - cl * mref1_, neg2_ = 0.0f - cl * mref2_;                                  \
-      const float nk0_ = SEEDED ? neg1_ - SEED_F * ct0_ : neg1_;                                           \
-      const float nk1_ = SEEDED ? neg2_ - SEED_F * ct1_ : neg2_;                                           \
-      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
-        sf_[0][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[0][v_], ct0_, nk0_));                       \
-        psum0_ += sf_[0][v_];                                                                              \
-      }                                                                                                    \
-      _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                  \
-        sf_[1][v_] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf_[1][v_], ct1_, nk1_));                       \
-        psum1_ += sf_[1][v_];                                                                              \
-      }                                                                                                    \
+      nk0_ = ((MODE) != 3 && SEEDED) ? neg1_ - SEED_F * ct0_ : neg1_;                                      \
+      nk1_ = slow_ ? -INFINITY : (((MODE) != 3 && SEEDED) ? neg2_ - SEED_F * ct1_ : neg2_);                \
+      /* exp2(carg0 + carg1) with carg1 counted unless slow; one of the two is 0 wherever a row has seen a   \
+         key (a non-slow first pass has no block-1 rescale, a redo pass's masked block 0 none at block 0), so \
+         this is the reference's corr0 or corr1; 1 in a lane whose max does not move */                      \
+      const float carg0_ = (m - mref1_) * cl, carg1_ = (m1_ - mref2_) * cl;                                \
+      resc_ = __ballot(need0_ || (!slow_ && need1_)) != 0;                                                 \
+      if (resc_) corr_ = __builtin_amdgcn_exp2f(carg0_ + (slow_ ? 0.0f : carg1_));                         \
+      m = slow_ ? m1_ : m2_;                                                                               \
+      negm = 0.0f - cl * (m == -INFINITY ? 0.0f : m);                                                      \
     }                                                                                                      \
-    /* slow: some lane moves its max at block 1 in a first pass, which then adds block 0 alone */          \
-    const bool slow_ = !(REDO) && __ballot(need1_) != 0;                                                   \
-    /* the rescale before this pass's MFMA: exp2(carg0 + carg1) with carg1 counted unless slow; one of the    \
-       two is 0 wherever a row has seen a key (a non-slow first pass has no block-1 rescale, a redo pass's    \
-       masked block 0 none at block 0), so this is the reference's corr0 or corr1.  Taken only in the rare    \
-       passes in which some lane of the wave rescales (elsewhere it is exp2(0) = 1). */                       \
-    float corr_ = 1.0f;                                                                                    \
-    if (__ballot(need0_ || (!slow_ && need1_)) != 0) {                                                     \
-      corr_ = __builtin_amdgcn_exp2f(carg0_ + (slow_ ? 0.0f : carg1_));                                    \
+    /* p = exp2(arg); each block's fp32 sum starts from its first p (0 + p is p) */                        \
+    float psum0_, psum1_;                                                                                  \
+    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
+      sf_[0][v_] = __builtin_amdgcn_exp2f((MODE) == 3 ? sf_[0][v_] + nk0_                                  \
+                                                      : __builtin_fmaf(sf_[0][v_], ct0_, nk0_));           \
+      psum0_ = v_ == 0 ? sf_[0][0] : psum0_ + sf_[0][v_];                                                  \
+    }                                                                                                      \
+    _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
+      sf_[1][v_] = __builtin_amdgcn_exp2f((MODE) == 3 ? sf_[1][v_] + nk1_                                  \
+                                                      : __builtin_fmaf(sf_[1][v_], ct1_, nk1_));           \
+      psum1_ = v_ == 0 ? sf_[1][0] : psum1_ + sf_[1][v_];                                                  \
+    }                                                                                                      \
+    if (resc_) {                                                                                           \
       _Pragma("unroll") for (int i_ = 0; i_ < NPV; ++i_)                                                   \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) o[i_][v_] *= corr_;                              \
     }                                                                                                      \
-    l = (corr_ * l + psum0_) + (slow_ ? 0.0f : psum1_);                                                    \
-    m = slow_ ? m1_ : m2_;                                                                                 \
+    l = (corr_ * l + psum0_) + psum1_;                                                                     \
     _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                     \
       const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                         \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);        \
-    }                                                                                                      \
-    /* bytes 16-31 of the B operand are block 1's keys (the V8T key order) */                               \
-    if (slow_) {                                                                                           \
-      pb[4] = 0;                                                                                           \
-      pb[5] = 0;                                                                                           \
-      pb[6] = 0;                                                                                           \
-      pb[7] = 0;                                                                                           \
     }                                                                                                      \
     _Pragma("unroll") for (int j_ = 0; j_ < NPV; ++j_) {                                                   \
       const v4i a0_ = *reinterpret_cast<const v4i*>(vt_ + vo0 + j_ * 32 * BN);                             \
