@@ -147,7 +147,12 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   constexpr uint32_t SEED_BITS = SEEDED ? 0x3E22F983u : 0u;
   constexpr float SEED_F = __builtin_bit_cast(float, SEED_BITS);
   constexpr float SSCALE = SEEDED ? 67108864.0f : 1.0f;  // 2^26
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][TILE];
+  // K / V tile buffers: three where they fit (the unmasked loops prefetch two tiles ahead, which hides the direct
+  // loads' latency behind two tiles of arithmetic), two for head dim 256 (3 x 32 KiB per workgroup would leave room
+  // for one workgroup per CU) and for the mask variant (whose loops prefetch one tile ahead)
+  constexpr int NBUF = (!MASK && D <= 128) ? 3 : 2;
+  constexpr int LPT = KLOADS + VLOADS;  // direct loads per wave and tile
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NBUF][TILE];
 
   // ---- work decode.  Dense: blocks [0, n_full) own whole query tiles (XCD-grouped); each later block owns one of
   // the `chunks` key ranges of a split tile.  VARLEN: the tile table. ----
@@ -299,6 +304,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   v4i bw_none[4] = {};  // the bias argument of the tile bodies without an additive mask (never read)
 
   // One tile: S^T = K Q^T (int8 MFMA), online softmax with the reference's lazy rescale, O^T += V^T P^T (fp8 MFMA).
+  // The wave raises its issue priority over each run of MFMAs, so that a wave with MFMAs ready feeds the matrix
+  // core ahead of the softmax arithmetic of the SIMD's other waves.
   // MODE 0: every key visible; 1: keys beyond the causal / padding bound masked; 2: keys whose bit of MW is clear
   // masked (MW = the lane's mask word of the tile); 3: the additive mask values BW (the lane's 32 16-bit values,
   // input dtype, -inf = masked) added in log2 units, with the row max taken over the biased logits.
@@ -316,9 +323,10 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
 #define SAGE_TILE(T, MODE, MW, BW, REDO)                                                                       \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
-    const uint8_t* kt_ = smem[t_ & 1];                                                                     \
-    const uint8_t* vt_ = smem[t_ & 1] + KTILE;                                                             \
+    const uint8_t* kt_ = smem[t_ % NBUF];                                                                  \
+    const uint8_t* vt_ = smem[t_ % NBUF] + KTILE;                                                          \
     v16i s_[2];                                                                                            \
+    __builtin_amdgcn_s_setprio(1);                                                                         \
     _Pragma("unroll") for (int i_ = 0; i_ < NQK; ++i_) {                                                   \
       const v4i k0_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_]);                                         \
       const v4i k1_ = *reinterpret_cast<const v4i*>(kt_ + ko[i_] + 32 * D);                                \
@@ -326,6 +334,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       s_[1] = i_ == 0 ? mfma_i8_seeded<SEEDED>(k1_, qa[i_])                                                \
                       : __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i_], s_[1], 0, 0, 0);                \
     }                                                                                                      \
+    __builtin_amdgcn_s_setprio(0);                                                                         \
     float sf_[2][16];                                                                                      \
     _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                    \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_)                                                    \
@@ -369,8 +378,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           if (kb_) tm1_ = fmaxf(tm1_, sf_[kb_][v_]);                                                       \
           else tm0_ = fmaxf(tm0_, sf_[kb_][v_]);                                                           \
         }                                                                                                  \
-      bm0_ = fmaxf(tm0_, xor32_f32(tm0_));                                                                 \
-      bm1_ = fmaxf(tm1_, xor32_f32(tm1_));                                                                 \
+      bm0_ = max_xor32_f32(tm0_);                                                                          \
+      bm1_ = max_xor32_f32(tm1_);                                                                          \
     } else {                                                                                               \
       float mx0_, mx1_;                                                                                    \
       if (SEEDED) {                                                                                        \
@@ -381,8 +390,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                    \
           mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                    \
         }                                                                                                  \
-        mx0_ = __int_as_float(max(mi0_, xor32_i32(mi0_)));                                                 \
-        mx1_ = __int_as_float(max(mi1_, xor32_i32(mi1_)));                                                 \
+        mx0_ = __int_as_float(max_xor32_i32(mi0_));                                                        \
+        mx1_ = __int_as_float(max_xor32_i32(mi1_));                                                        \
       } else {                                                                                             \
         mx0_ = sf_[0][0];                                                                                  \
         mx1_ = sf_[1][0];                                                                                  \
@@ -390,8 +399,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                  \
           mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                  \
         }                                                                                                  \
-        mx0_ = fmaxf(mx0_, xor32_f32(mx0_));                                                               \
-        mx1_ = fmaxf(mx1_, xor32_f32(mx1_));                                                               \
+        mx0_ = max_xor32_f32(mx0_);                                                                        \
+        mx1_ = max_xor32_f32(mx1_);                                                                        \
       }                                                                                                    \
       bm0_ = SEEDED ? (mx0_ - SEED_F) * ks0_ : mx0_ * ks0_;                                                \
       bm1_ = SEEDED ? (mx1_ - SEED_F) * ks1_ : mx1_ * ks1_;                                                \
@@ -471,12 +480,14 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);        \
     }                                                                                                      \
+    __builtin_amdgcn_s_setprio(1);                                                                         \
     _Pragma("unroll") for (int j_ = 0; j_ < NPV; ++j_) {                                                   \
       const v4i a0_ = *reinterpret_cast<const v4i*>(vt_ + vo0 + j_ * 32 * BN);                             \
       const v4i a1_ = *reinterpret_cast<const v4i*>(vt_ + vo1 + j_ * 32 * BN);                             \
       const v8i va_ = {a0_[0], a0_[1], a0_[2], a0_[3], a1_[0], a1_[1], a1_[2], a1_[3]};                    \
       o[j_] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va_, pb, o[j_], 0, 0, 0, 0, 0, 0);           \
     }                                                                                                      \
+    __builtin_amdgcn_s_setprio(0);                                                                         \
     redo_ = slow_;                                                                                         \
   } while (0)
 
@@ -508,9 +519,15 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   v16i seed16;
 #pragma unroll
   for (int v = 0; v < 16; ++v) seed16[v] = (int)SEED_BITS;
-  if (t_lo < t_hi) SAGE_ISSUE_TILE(t_lo, t_lo & 1);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  // the first tile (and, with three buffers, the second) in flight; wait for the first
+  if (t_lo < t_hi) SAGE_ISSUE_TILE(t_lo, t_lo % NBUF);
+  if (NBUF == 3 && t_lo + 1 < t_hi) {
+    SAGE_ISSUE_TILE(t_lo + 1, (t_lo + 1) % NBUF);
+    wait_vmcnt<LPT>();
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  tile_barrier();
   int t = t_lo;
   if (MASK) {
     // per wave and tile: skip (class 0), the mask-free body (1) or the bit-masked body (2).  Runs of tiles of
@@ -570,17 +587,24 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       }
     }
   } else {
+    // tile t + NBUF - 1 goes into the buffer tile t - 1 used, which every wave left at the last barrier; the end of
+    // tile t waits for tile t + 1 (all but the LPT loads of tile t + 2 when those were issued: loads complete in order)
+    constexpr int PF = NBUF - 1;
     for (; t < t_mask; ++t) {
-      if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+      const bool ahead = t + PF < t_hi;
+      if (ahead) SAGE_ISSUE_TILE(t + PF, (t + PF) % NBUF);
       SAGE_TILE_PASSES(t, 0, 0u, bw_none);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
+      if (PF == 2 && ahead) wait_vmcnt<LPT>();
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      tile_barrier();
     }
     for (; t < t_hi; ++t) {
-      if (t + 1 < t_hi) SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
+      const bool ahead = t + PF < t_hi;
+      if (ahead) SAGE_ISSUE_TILE(t + PF, (t + PF) % NBUF);
       SAGE_TILE_PASSES(t, 1, 0u, bw_none);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
+      if (PF == 2 && ahead) wait_vmcnt<LPT>();
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      tile_barrier();
     }
   }
 #undef SAGE_ISSUE_TILE
@@ -588,7 +612,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
 #undef SAGE_TILE_PASSES
 
   // ---- epilogue ----
-  const float lt = l + xor32_f32(l);
+  const float lt = add_xor32_f32(l);
   if (split) {
     // partial state of this key range (workspace layout at ws_ml_offset), merged by attn_merge_kernel
     const int q = wave * 32 + ln;

@@ -63,12 +63,37 @@ template <int CTRL> __device__ __forceinline__ double dpp_f64(double x) {
   const int phi = __builtin_amdgcn_mov_dpp(hi, CTRL, 0xF, 0xF, false);
   return __hiloint2double(phi, plo);
 }
-// value held by lane (lane ^ 32)
-__device__ __forceinline__ int xor32_i32(int x) {
-  const int lane = __lane_id();
-  return __builtin_amdgcn_ds_bpermute(((lane ^ 32) << 2), x);
+// Wait until at most N of this wave's vector memory operations are outstanding (they complete in issue order)
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 15, "vmcnt immediate");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-__device__ __forceinline__ float xor32_f32(float x) { return __int_as_float(xor32_i32(__float_as_int(x))); }
+// Workgroup barrier between K / V tiles.  The tile buffers are written only by direct global -> LDS loads, which
+// the loops wait for explicitly (vmcnt), and read by ds_reads, which complete before the tile's MFMAs use them; so
+// the barrier needs no memory fence.  __syncthreads()'s fence would make the compiler wait for every outstanding
+// direct load (vmcnt(0)), including the prefetch of a later tile.  The empty asm statements keep the compiler from
+// moving LDS accesses across the barrier.
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// Combine a value with the one held by lane (lane ^ 32), in every lane.  v_permlane32_swap_b32 on two copies of x
+// leaves r[0] = x[lane mod 32] and r[1] = x[lane mod 32 + 32] in every lane: one VALU op, where a ds_bpermute would
+// be an LDS round trip.  max and + are commutative, so both halves get the same bits in the same order as
+// op(x[lane], x[lane ^ 32]) would give them.
+__device__ __forceinline__ int max_xor32_i32(int x) {
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+__device__ __forceinline__ float max_xor32_f32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor32_f32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // ---- Hadamard (float64 FWHT) -----------------------------------------------------------------------------------
 // x holds EPL consecutive elements of a row whose other slices sit in the 1 / 2 / 4 neighbouring lanes of a quad

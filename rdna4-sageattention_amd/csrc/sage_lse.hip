@@ -154,7 +154,7 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
     for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sv[0][v]);
 #pragma unroll
     for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sv[1][v]);
-    mx = fmaxf(mx, xor32_f32(mx));
+    mx = max_xor32_f32(mx);
     const float m_new = fmaxf(m, mx);
     const float corr = __builtin_amdgcn_exp2f((m - m_new) * c);  // m = -inf on the first tile: corr = 0
     const float neg = 0.0f - m_new * c;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(l) : : "memory");
     __syncthreads();
   }
-  const float lt = l + xor32_f32(l);
+  const float lt = add_xor32_f32(l);
   if (qvalid && hf == 0) lse[(int64_t)bh * Sq + qrow] = 0.69314718055994531f * (m * c + __log2f(lt));
 }
 
