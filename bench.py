@@ -105,11 +105,16 @@ def cpu_baseline(cfg, target_s=15.0):
     }
 
 
+PROFILE_STEMS = {"2": "flux_config2", "3": "wan14b_config3", "4": "hunyuan_config4", "5a": "causal_gqa_config5a",
+                 "5b": "causal_gqa_d64_config5b"}
+
+
 def profiled_traffic(cfg_key):
     """HBM bytes per attention call (attention kernel + merge of split tiles) from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (config 2)."""
-    f = ROOT / "profiles" / "flux_config2_hbm_traffic.md"
-    if cfg_key != "2" or not f.exists():
+    FETCH_SIZE / WRITE_SIZE summary of this configuration."""
+    stem = PROFILE_STEMS.get(cfg_key)
+    f = ROOT / "profiles" / f"{stem}_profile.md" if stem else None
+    if f is None or not f.exists():
         return None, None
     for line in f.read_text().splitlines():
         if line.startswith("attention traffic_bytes_per_call:"):
