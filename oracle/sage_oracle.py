@@ -78,9 +78,9 @@ KERNEL_TILE = 64
 
 def seeded(d_layout: int) -> bool:
     """Whether the gfx950 kernel reads its scores seeded (F = c + S * 2^-26) for a layout of d_layout channels:
-    c + S * 2^-26 stays in c's binade [1/8, 1/4) for -2,292,099 <= S < 6,097,183, i.e. |S| <= 127^2 * d_layout for
-    d_layout <= 128.  Head dim 256 (|S| up to 4,129,024) converts S to fp32 instead (F = S), the reference's
-    arithmetic."""
+    c + S * 2^-26 is exact (inside c's binade [1/8, 1/4], whose ends read right) for -2,292,099 <= S <= 6,096,509,
+    i.e. |S| <= 127^2 * d_layout for d_layout <= 128.  Head dim 256 (|S| up to 4,129,024) converts S to fp32
+    instead (F = S), the reference's arithmetic."""
     return 127 * 127 * d_layout < 2292099
 
 

@@ -11,10 +11,10 @@
 //     l      = corr * l + sum_j p_ij (fp32 p);  O = need ? O * corr : O;  O += e4m3(p) V8;  corr = exp2((m - m_new) cl)
 //   out    = (O * ((1/448) / l)) * VS
 // Scores.  Head dims up to 128 seed the QK accumulators with the bit pattern of c = fp32(1 / (2 pi)) = 0x3E22F983,
-// an inline constant of the MFMA (no registers hold the seed): since -2,292,099 <= S < 6,097,183 there, the int32
-// result stays inside c's binade [1/8, 1/4), whose ulp is 2^-26, so read as fp32 it is F = c + S * 2^-26 exactly and
-// needs no conversion; nk = -(cl * m_new) - fp32(c * ct), so F * ct + nk equals S * ct - cl * m_new up to the
-// rounding of nk.  Those kernels keep cl scaled by 2^26 and m by 2^-26 (powers of two: every product and difference
+// an inline constant of the MFMA (no registers hold the seed): since -2,292,099 <= S <= 6,096,509 there, the int32
+// result stays inside c's binade [1/8, 1/4] (ulp 2^-26; its ends read right), so read as fp32 it is
+// F = c + S * 2^-26 and needs no conversion; nk = -(cl * m_new) - fp32(c * ct), so F * ct + nk equals
+// S * ct - cl * m_new up to the rounding of nk.  Those kernels keep cl scaled by 2^26 and m by 2^-26 (powers of two: every product and difference
 // of the math above is the same bits, scaled).  Head dim 256 reaches |S| = 4,129,024, outside that binade, so its
 // accumulators start at 0 and F = fp32(S) (v_cvt_f32_i32), nk = -(cl * m_new): the reference's arithmetic.
 //
@@ -92,8 +92,8 @@ template <bool SEEDED> __device__ __forceinline__ v16i mfma_i8_seeded(v4i a, v4i
 }
 
 // Whether the QK accumulators of a kernel covering `da` channels start at the seed c = fp32(1 / (2 pi)).  The int32
-// sum read as fp32 is c + S * 2^-26 exactly while it stays inside c's binade [1/8, 1/4), i.e. for
-// -2,292,099 <= S < 6,097,183 (c = 10,680,707 * 2^-26).  |S| <= 127^2 * da: 1,032,256 (64), 1,548,384 (96, zero
+// sum read as fp32 is c + S * 2^-26 exactly while it stays inside c's binade [1/8, 1/4] (the ends read right), i.e. for
+// -2,292,099 <= S <= 6,096,509 (c = 10,680,707 * 2^-26).  |S| <= 127^2 * da: 1,032,256 (64), 1,548,384 (96, zero
 // padded), 2,064,512 (128) fit; head dim 256 reaches 4,129,024 and converts S with v_cvt_f32_i32 instead.
 __host__ __device__ constexpr bool attn_seeded(int da) { return 127 * 127 * da < 2292099; }
 

@@ -615,3 +615,22 @@ def test_attention_on_sampled_query_rows(causal):
     part = orc.attention(np.ascontiguousarray(q8[:, :, sel]), np.ascontiguousarray(qs[:, :, sel]), k8, ks, v8, vs,
                          260, causal=causal, kv_split=(3, rows_split[:, :, sel]), q_rows=sel, seq_q=200)
     assert np.array_equal(part, full[:, :, sel])
+
+
+def test_seed_binade_holds_the_scores_of_each_head_dim():
+    """The seeded read F = c + S * 2^-26 is exact exactly while the int32 sum stays in c's binade: check the two
+    ends by the int32 pattern arithmetic the kernel relies on, and which head dims the kernels seed."""
+    c_bits = int(np.array([orc.SEED], dtype=np.float32).view(np.uint32)[0])
+    assert c_bits == 0x3E22F983 and abs(orc.SEED - 1 / (2 * math.pi)) < 2.0 ** -26
+
+    def read(s):  # the accumulator's int32 bits read as fp32
+        return float(np.array([c_bits + s], dtype=np.int64).astype(np.uint32).view(np.float32)[0])
+
+    # the ends: 1/8 and 1/4 themselves read right (mantissa 0); one step further the ulp changes
+    for s in (-2292099, -1, 0, 1, 2064512, 6096509):
+        assert Fraction(read(s)) == Fraction(orc.SEED) + Fraction(s, 2 ** 26), s
+    for s in (-2292100, -4129024, 6096510):
+        assert Fraction(read(s)) != Fraction(orc.SEED) + Fraction(s, 2 ** 26), s
+    # |S| <= 127^2 * (channels one MFMA sum covers); d96 runs 96 nonzero channels of the 128 layout
+    assert orc.seeded(64) and orc.seeded(96) and orc.seeded(128) and not orc.seeded(256)
+    assert 127 * 127 * 128 <= 2292099 < 127 * 127 * 256
