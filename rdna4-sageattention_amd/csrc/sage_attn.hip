@@ -361,12 +361,13 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     }                                                                                                      \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
-    /* the two 32-key blocks' row maxima: MODE 3 in log2 units of the biased logits t (kept in sf_), else in  \
-       m's units, fp32(max S * ks) (scaled by 2^-26 when seeded: mx - c is exact) */                       \
-    float bm0_, bm1_;                                                                                      \
+    /* the two 32-key blocks' row maxima, one per lane half (block hf's, for row ln): MODE 3 in log2 units of the \
+       biased logits t (kept in sf_), else in m's units, fp32(max S * ks) (scaled by 2^-26 when seeded: mx - c is \
+       exact).  One lane exchange gives block 0's max in lanes 0-31 and block 1's in lanes 32-63. */       \
+    float bmh_;                                                                                            \
     if ((MODE) == 3) {                                                                                     \
-      /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))) (b = -inf for a masked key gives -inf); the lazy         \
-         rescale compares a block's max of t with m * cl and keeps m in S * ks units (m_new = m_cand / cl) */  \
+      /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))) (b = -inf for a masked key gives -inf); the lazy     \
+         rescale compares a block's max of t with m * cl and keeps m in S * ks units (m_new = m_cand / cl) */ \
       const float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;      \
       float tm0_ = -INFINITY, tm1_ = -INFINITY;                                                            \
       _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
@@ -378,39 +379,33 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           if (kb_) tm1_ = fmaxf(tm1_, sf_[kb_][v_]);                                                       \
           else tm0_ = fmaxf(tm0_, sf_[kb_][v_]);                                                           \
         }                                                                                                  \
-      bm0_ = max_xor32_f32(tm0_);                                                                          \
-      bm1_ = max_xor32_f32(tm1_);                                                                          \
+      bmh_ = halves_max_f32(tm0_, tm1_);                                                                   \
     } else {                                                                                               \
-      float mx0_, mx1_;                                                                                    \
+      float mxh_;                                                                                          \
       if (SEEDED) {                                                                                        \
-        /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose    \
-           int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */        \
-        int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                           \
+        /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose \
+           int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */       \
+        int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                            \
         _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                \
           mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                    \
           mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                    \
         }                                                                                                  \
-        mx0_ = __int_as_float(max_xor32_i32(mi0_));                                                        \
-        mx1_ = __int_as_float(max_xor32_i32(mi1_));                                                        \
+        mxh_ = __int_as_float(halves_max_i32(mi0_, mi1_));                                                 \
       } else {                                                                                             \
-        mx0_ = sf_[0][0];                                                                                  \
-        mx1_ = sf_[1][0];                                                                                  \
+        float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                          \
         _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                \
           mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                  \
           mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                  \
         }                                                                                                  \
-        mx0_ = max_xor32_f32(mx0_);                                                                        \
-        mx1_ = max_xor32_f32(mx1_);                                                                        \
+        mxh_ = halves_max_f32(mx0_, mx1_);                                                                 \
       }                                                                                                    \
-      bm0_ = SEEDED ? (mx0_ - SEED_F) * ks0_ : mx0_ * ks0_;                                                \
-      bm1_ = SEEDED ? (mx1_ - SEED_F) * ks1_ : mx1_ * ks1_;                                                \
+      const float ksh_ = hf ? ks1_ : ks0_;                                                                 \
+      bmh_ = SEEDED ? (mxh_ - SEED_F) * ksh_ : mxh_ * ksh_;                                                \
     }                                                                                                      \
-    /* Does some lane of the wave move its max at either block?  Subtraction and the product with cl > 0 are  \
-       monotonic, so a larger block max can only raise the test: with the larger of the two below the         \
-       threshold, neither block's decision fires (and an -inf max against m = -inf gives NaN, false, as the   \
-       per-block test does).  Then m stays, and so does the exponent offset negm = -(cl * m_ref). */         \
-    const bool any_ = __ballot((MODE) == 3 ? (fmaxf(bm0_, bm1_) - m * cl) > 8.0f                          \
-                                           : (fmaxf(bm0_, bm1_) - m) * cl > 8.0f) != 0;                   \
+    /* Does some lane of the wave move its max at either block?  The ballot over both lane halves covers both \
+       blocks of every row (an -inf max against m = -inf gives NaN, false, as the per-block test does).  Then \
+       m stays, and so does the exponent offset negm = -(cl * m_ref). */                                   \
+    const bool any_ = __ballot((MODE) == 3 ? (bmh_ - m * cl) > 8.0f : (bmh_ - m) * cl > 8.0f) != 0;        \
     float nk0_, nk1_;       /* the blocks' exponent offsets (MODE 3: added to t) */                        \
     float corr_ = 1.0f;     /* the rescale before this pass's MFMA */                                      \
     bool slow_ = false;     /* some lane moves its max at block 1 in a first pass: block 1 waits for pass 1 */ \
@@ -420,6 +415,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       nk1_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct1_ : negm;                                        \
     } else {                                                                                               \
       /* the reference's decisions, block 0 against m, block 1 against the max m1 block 0 left */          \
+      float bm0_, bm1_;                                                                                    \
+      halves_split_f32(bmh_, bm0_, bm1_);                                                                  \
       bool need0_, need1_;                                                                                 \
       float m1_, m2_;                                                                                      \
       if ((MODE) == 3) {                                                                                   \

@@ -90,6 +90,23 @@ __device__ __forceinline__ float max_xor32_f32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// One v_permlane32_swap_b32 on two per-lane partial maxima a (block 0) and b (block 1) of rows held by lanes l and
+// l ^ 32: the result is row (l mod 32)'s full maximum of a in lanes 0-31 and of b in lanes 32-63.
+__device__ __forceinline__ int halves_max_i32(int a, int b) {
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)a, (unsigned)b, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+__device__ __forceinline__ float halves_max_f32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// The inverse exchange: from x (block 0's value in lanes 0-31, block 1's in lanes 32-63, per row l mod 32), both
+// values in every lane: lo = block 0's, hi = block 1's.
+__device__ __forceinline__ void halves_split_f32(float x, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float add_xor32_f32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);

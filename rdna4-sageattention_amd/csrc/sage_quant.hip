@@ -277,23 +277,24 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
   constexpr int RPI = 256 / LPR;  // rows per pass
   const int c8 = threadIdx.x % LPR, r0 = threadIdx.x / LPR;
   if (c8 * 8 >= D) nvalid = 0;  // padding channels of D = 96: zeros
-  // all of the thread's 128 / RPI rows in flight first: they do not depend on the channel maxima reduced below
+  // The channel maxima are loaded first and the thread's 128 / RPI rows of V right behind them: loads complete in
+  // order, so the maxima's reduction waits for its own few loads and runs while the rows are in flight.
   const uint16_t* vbase = base + c8 * 8;
-  uint4 wv[128 / RPI];
-#pragma unroll
-  for (int g = 0; g < 128 / RPI; ++g) {
-    const int row = local0 + r0 + g * RPI;
-    const bool ok = row < nvalid;
-    wv[g] = load16_or_zero(ok ? vbase + (int64_t)row * vss : base, ok);  // base: row 0, channel 0 of the sequence
-  }
   float am[8];
+  uint4 wv[128 / RPI];
   if (vchunks == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) am[i] = am_src[c8 * 8 + i];
+    for (int i = 0; i < 8; ++i) am[i] = am_src[c8 * 8 + i];  // VS may be only 4-byte aligned (sage_quant_kv)
+#pragma unroll
+    for (int g = 0; g < 128 / RPI; ++g) {
+      const int row = local0 + r0 + g * RPI;
+      const bool ok = row < nvalid;
+      wv[g] = load16_or_zero(ok ? vbase + (int64_t)row * vss : base, ok);  // base: row 0, channel 0 of the sequence
+    }
   } else {
     // the per-chunk maxima are reduced once per block: thread (4-channel group cg, slice cs) takes the maximum of
-    // chunks cs, cs + NSL, ... (all its loads in flight), the slices meet in LDS, and one row of threads reduces
-    // them (and stores VS when vs_out is set); every thread then reads its 8 channels.
+    // chunks cs, cs + NSL, ..., the slices meet in LDS, and one row of threads reduces them (and stores VS when
+    // vs_out is set); every thread then reads its 8 channels.
     constexpr int NCG = DP / 4, NSL = 256 / NCG, PER = (V_AMAX_CHUNKS + NSL - 1) / NSL;
     __shared__ __attribute__((aligned(16))) float vpart_lds[NSL][DP];
     const int cg = threadIdx.x % NCG, cs = threadIdx.x / NCG;
@@ -301,6 +302,12 @@ __device__ __forceinline__ void quant_v128_core(const uint16_t* __restrict__ bas
 #pragma unroll
     for (int i = 0; i < PER; ++i)  // chunks past the last one repeat it, which a maximum does not notice
       pc[i] = *reinterpret_cast<const v4f*>(am_src + (int64_t)min(cs + i * NSL, vchunks - 1) * DP + 4 * cg);
+#pragma unroll
+    for (int g = 0; g < 128 / RPI; ++g) {
+      const int row = local0 + r0 + g * RPI;
+      const bool ok = row < nvalid;
+      wv[g] = load16_or_zero(ok ? vbase + (int64_t)row * vss : base, ok);
+    }
     v4f m4 = pc[0];
 #pragma unroll
     for (int i = 1; i < PER; ++i)
