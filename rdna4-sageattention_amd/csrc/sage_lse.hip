@@ -10,6 +10,8 @@
 // with lane l ^ 32.  Statistics are exact online max / sum in the log2 domain (no lazy threshold: there is no output
 // accumulator to rescale): m = max_j s_ij, l = sum_j 2^((s_ij - m) * c) with c = sm_scale * log2(e), and
 // lse = ln 2 * (m * c + log2 l).  Causal masks are bottom-right aligned (Sq <= Skv).
+#include <type_traits>
+
 #include "sage_common.h"
 #include "sage_host.h"
 
@@ -119,11 +121,11 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
   for (int i = 0; i < NK; ++i) ko[i] = ln * ROWB + lse_swz<KCH>(ln, 2 * i + hf) * 16;
 
   float m = -INFINITY, l = 0.0f;
-  issue(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
+  // One tile: S^T from the LDS buffer, the MASKED body clears keys past Skv and (causal) past the row's diagonal.
+  // The two bodies sit in two loops (tiles before t_mask need no mask for any row of the wave): with the mask test
+  // in one loop the compiler turns the masking into compares and selects on every tile.
+  auto tile = [&](int t, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
     const uint8_t* kt = smem[t & 1];
     v16f s0 = {}, s1 = {};
 #pragma unroll
@@ -139,15 +141,14 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
       sv[0][v] = s0[v];
       sv[1][v] = s1[v];
     }
-    const int kstart = t * BN;
-    if (kstart + BN > Skv || (CAUSAL && kstart + BN - 1 > q0 + off)) {
+    if constexpr (MASKED) {
+      // element (kb, v) holds key t * 64 + 4 hf + (32 kb + 8 (v / 4) + v % 4): visible iff that offset <= lim
+      const int lim = (CAUSAL ? min(Skv - 1, qr + off) : Skv - 1) - (t * BN + 4 * hf);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = kstart + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
-          if (key >= Skv || (CAUSAL && key > qr + off)) sv[kb][v] = -INFINITY;
-        }
+        for (int v = 0; v < 16; ++v)
+          if (32 * kb + 8 * (v >> 2) + (v & 3) > lim) sv[kb][v] = -INFINITY;
     }
     float mx = sv[0][0];
 #pragma unroll
@@ -169,6 +170,22 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
     // the operand the scheduler may hoist the wait into the middle of the tile)
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(l) : : "memory");
     __syncthreads();
+  };
+  // tiles before t_mask end below Skv and (causal) at or before the wave's first row's diagonal
+  int t_mask = Skv / BN;
+  if (CAUSAL) t_mask = min(t_mask, max(0, (q0 + off + 1) / BN));
+  t_mask = min(t_mask, ntiles);
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  int t = 0;
+  for (; t < t_mask; ++t) {
+    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
+    tile(t, std::false_type{});
+  }
+  for (; t < ntiles; ++t) {
+    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
+    tile(t, std::true_type{});
   }
   const float lt = add_xor32_f32(l);
   if (qvalid && hf == 0) lse[(int64_t)bh * Sq + qrow] = 0.69314718055994531f * (m * c + __log2f(lt));
