@@ -171,8 +171,18 @@ def test_sageattn_routes_bool_masks_to_the_kernel(dev, monkeypatch):
     fmask = torch.zeros(1, 1, 1, 1024, device=dev, dtype=torch.bfloat16)
     fmask[..., 900:] = float("-inf")
     assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=fmask), kern)   # the same mask as an additive one
+    # a query row that sees no key: 0 on the kernel route, torch SDPA's own output (NaN for its math path) with
+    # the reference's routing; every other row is the same on both routes as above
+    rowmask = torch.ones(1, 1, 1024, 1024, dtype=torch.bool, device=dev)
+    rowmask[..., 7, :] = False
+    kern_rows = cdna4_sage.sageattn(q, k, v, attn_mask=rowmask)
+    assert (kern_rows[:, :, 7] == 0).all() and torch.isfinite(kern_rows).all()
     monkeypatch.setattr(cdna4_sage, "NATIVE_MASK", False)
     assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=mask), cdna4_sage._torch_sdpa(q, k, v, attn_mask=mask))
+    sdpa_rows = cdna4_sage.sageattn(q, k, v, attn_mask=rowmask)
+    ref_rows = cdna4_sage._torch_sdpa(q, k, v, attn_mask=rowmask)
+    assert torch.equal(sdpa_rows.isnan(), ref_rows.isnan())
+    assert torch.equal(torch.nan_to_num(sdpa_rows), torch.nan_to_num(ref_rows))
 
 
 def _alibi(H, Sq, Skv, slope=0.03):
