@@ -82,10 +82,6 @@ __device__ __forceinline__ void tile_barrier() {
 // leaves r[0] = x[lane mod 32] and r[1] = x[lane mod 32 + 32] in every lane: one VALU op, where a ds_bpermute would
 // be an LDS round trip.  max and + are commutative, so both halves get the same bits in the same order as
 // op(x[lane], x[lane ^ 32]) would give them.
-__device__ __forceinline__ int max_xor32_i32(int x) {
-  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
-  return max((int)r[0], (int)r[1]);
-}
 __device__ __forceinline__ float max_xor32_f32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
