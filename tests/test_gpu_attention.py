@@ -41,6 +41,11 @@ CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 2, 2, 300, 500, 256, torch.bfloat16, "HND", False),    # head_dim 256: block-diagonal rotation
     (2, 2, 1, 200, 200, 256, torch.float16, "NHD", True),
     (1, 8, 8, 1024, 1024, 256, torch.bfloat16, "HND", False),  # several split key ranges
+    # one to three key tiles: the prologue loads the first tile and prefetches the second when there is one
+    (1, 2, 2, 96, 33, 128, torch.bfloat16, "HND", False),      # one partial tile
+    (1, 2, 2, 200, 100, 64, torch.float16, "HND", False),      # a whole tile and a partial one
+    (1, 2, 2, 128, 128, 128, torch.bfloat16, "NHD", True),     # two whole tiles, causal
+    (2, 2, 1, 70, 190, 128, torch.bfloat16, "HND", True),      # three tiles, causal with q_len < kv_len
 ]
 
 

@@ -17,6 +17,10 @@ CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 2, 2, 130, 777, 128, torch.float16, "HND", True),    # bottom-right causal with q_len < kv_len
     (3, 2, 2, 77, 1031, 128, torch.bfloat16, "NHD", False),
     (1, 3, 3, 1, 64, 128, torch.bfloat16, "HND", False),
+    # short key ranges: the mask-free loop may run no tile at all
+    (1, 2, 2, 96, 33, 128, torch.bfloat16, "HND", False),
+    (1, 2, 2, 128, 128, 64, torch.float16, "NHD", True),
+    (2, 2, 1, 70, 190, 128, torch.bfloat16, "HND", True),
 ]
 
 
