@@ -137,7 +137,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported (each call is a single-device "
-              "op; multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "op on one GPU; sharding heads or sequences over several GPUs is not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -67,8 +67,8 @@ KV_BLOCK = 32          # one K scale per 32 keys (kernel_build/build_kernels.py:
 E4M3_MAX = 448.0
 RESCALE_THRESHOLD = 8.0  # make_sage.py:219-225: keep a stale max until it is exceeded by 2^8
 LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
-# fp32(1 / (2 pi)) = 0x3E22F983, the gfx950 kernel's seed of the QK accumulators: c + S * 2^-26 is exact for
-# |S| < 2^21 (the binade [1/8, 1/4) has ulp 2^-26), so the int32 sum read as fp32 needs no conversion
+# fp32(1 / (2 pi)) = 0x3E22F983, the gfx950 kernel's seed of the QK accumulators for head dims up to 128: the int32
+# sum read as fp32 is c + S * 2^-26 exactly for -2,292,099 <= S <= 6,096,509 (see seeded()), so it needs no conversion
 SEED = float(np.array([0x3E22F983], dtype=np.uint32).view(np.float32)[0])
 SEED_ULP = 2.0 ** -26
 # the gfx950 kernel's key tile: split key ranges and the classes of additive masks are per 64-key tile, whatever the

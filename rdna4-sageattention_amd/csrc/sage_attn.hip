@@ -14,17 +14,17 @@
 // an inline constant of the MFMA (no registers hold the seed): since -2,292,099 <= S <= 6,096,509 there, the int32
 // result stays inside c's binade [1/8, 1/4] (ulp 2^-26; its ends read right), so read as fp32 it is
 // F = c + S * 2^-26 and needs no conversion; nk = -(cl * m_new) - fp32(c * ct), so F * ct + nk equals
-// S * ct - cl * m_new up to the rounding of nk.  Those kernels keep cl scaled by 2^26 and m by 2^-26 (powers of two: every product and difference
-// of the math above is the same bits, scaled).  Head dim 256 reaches |S| = 4,129,024, outside that binade, so its
+// S * ct - cl * m_new up to the rounding of nk.  Those kernels keep cl scaled by 2^26 and m by 2^-26 (powers of
+// two: every product and difference of the math above is the same bits, scaled).  Head dim 256 reaches |S| = 4,129,024, outside that binade, so its
 // accumulators start at 0 and F = fp32(S) (v_cvt_f32_i32), nk = -(cl * m_new): the reference's arithmetic.
 //
 // gfx950 mapping.  A workgroup owns 128 query rows (4 waves x 32) of one (batch, head) and walks the KV sequence
-// in 64-key tiles staged in LDS (double buffered; the next tile's global loads are in flight while the current
-// one is computed).  Per wave and tile:
+// in 64-key tiles staged in LDS by direct global -> LDS loads (three buffers at head dims up to 128, the loads of the
+// next two tiles in flight while one is computed; two at 256 and in the mask variant).  Per wave and tile:
 //   * S^T = K Q^T with v_mfma_i32_32x32x32_i8: A = 32 keys x 32 dims of K (LDS), B = 32 dims x 32 queries of Q
 //     (registers for the whole kernel).  The 32x32 accumulator gives lane l the query l % 32 and 16 keys
 //     8(v/4) + 4(l/32) + v%4 of the block (v = accumulator register), so row statistics need one exchange with lane
-//     l ^ 32 and no other cross-lane traffic.
+//     l ^ 32 (v_permlane32_swap) and no other cross-lane traffic.
 //   * The 2 x 16 probabilities of a lane, cast to E4M3 in register order, are exactly the lane's 32-byte B operand
 //     of v_mfma_f32_32x32x64_f8f6f4 for O^T = V^T P^T: B = 64 keys x 32 queries.  The A operand (32 channels x 64
 //     keys of V) must hold the same keys in the same byte order; the quantizer stores V8T with keys permuted inside

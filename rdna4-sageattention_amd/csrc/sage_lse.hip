@@ -4,7 +4,8 @@
 // accuracy, as the reference's fp32 matmul does.
 //
 // gfx950 mapping: a workgroup owns 128 query rows (4 waves x 32) of one (batch, head) and walks the keys in 64-key tiles
-// copied global -> LDS (direct loads, double buffered, 16-byte chunks XOR-swizzled by row).  Per wave and tile,
+// copied global -> LDS (direct loads, double buffered, 16-byte chunks XOR-swizzled by row; the tiles no row of a
+// wave needs masked run a mask-free body).  Per wave and tile,
 // S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = 32 keys x 16 dims of K from LDS, B = Q from registers.  The
 // accumulator gives lane l the query l % 32 and 16 keys of each 32-key block, so the row statistics need one exchange
 // with lane l ^ 32.  Statistics are exact online max / sum in the log2 domain (no lazy threshold: there is no output
