@@ -1,0 +1,80 @@
+"""A seeded sweep of random shapes through the kernel-forced entry against the CPU emulation of the reference's math
+(32-key lazy-rescale blocks, the kernel's split plan): batch, heads and GQA ratio, odd query / key lengths (one key
+tile to many, causal with q_len <= kv_len), head dims 64 / 96 / 128 / 256, bf16 / fp16, HND / NHD, an explicit
+sm_scale, input scales from 0.1 to 4 and outlier channels.  Same gates as the hand-picked cases: max-abs 2e-2 against
+the emulation, cosine 0.999 against float attention (where the reference math itself reaches it), and the share of
+output elements bit-equal to the emulation."""
+import numpy as np
+import pytest
+import torch
+
+import cdna4_sage
+from cdna4_sage import _capi
+from gpu_util import cosine, hnd_np, kv_split
+from oracle import sage_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+COS = 0.999
+SAME_BITS = {torch.bfloat16: 0.95, torch.float16: 0.85}
+
+
+def _cases(n=40, seed=20261202):
+    rng = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([64, 96, 128, 256]))
+        Hkv = int(rng.randint(1, 4))
+        H = Hkv * int(rng.choice([1, 2, 4]))
+        B = int(rng.randint(1, 3))
+        Skv = int(rng.choice([int(rng.randint(1, 130)), int(rng.randint(130, 1100))]))
+        causal = bool(rng.rand() < 0.4)
+        Sq = int(rng.randint(1, min(Skv, 600) + 1)) if causal else int(rng.randint(1, 600))
+        dt = torch.bfloat16 if rng.rand() < 0.6 else torch.float16
+        layout = "HND" if rng.rand() < 0.6 else "NHD"
+        sm = None if rng.rand() < 0.7 else float(rng.uniform(0.03, 0.2))
+        scale = float(np.exp(rng.uniform(np.log(0.1), np.log(4.0))))
+        outliers = bool(rng.rand() < 0.3)
+        out.append((i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, sm, scale, outliers))
+    return out
+
+
+CASES = _cases()
+
+
+def _ids(c):
+    i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, sm, scale, outl = c
+    return (f"{i}-B{B}H{H}/{Hkv}-{Sq}x{Skv}-d{D}-{'bf16' if dt == torch.bfloat16 else 'f16'}-{layout}"
+            f"{'-causal' if causal else ''}{'-sm' if sm else ''}{'-outl' if outl else ''}")
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+def test_random_shapes_vs_emulation(dev, case):
+    i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, sm, scale, outliers = case
+    g = torch.Generator().manual_seed(1000 + i)
+    q = torch.randn(B, H, Sq, D, generator=g) * scale
+    k = torch.randn(B, Hkv, Skv, D, generator=g) * scale
+    v = torch.randn(B, Hkv, Skv, D, generator=g)
+    if outliers:  # a few channels x10, as in activations with massive channels
+        ch = torch.randperm(D, generator=g)[:3]
+        q[..., ch] *= 10
+        k[..., ch] *= 10
+        v[..., ch[:1]] *= 10
+    q, k, v = (t.to(dt) for t in (q, k, v))
+    if layout == "NHD":
+        q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), tensor_layout=layout, sm_scale=sm, is_causal=causal)
+    assert out.shape == q.shape and out.dtype == dt
+    got = hnd_np(out, layout)
+    qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
+    q8, qs = orc.quant_q(qn, sm)
+    k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(Skv))
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, Skv, causal=causal, block_n=32,
+                        out_dtype="bf16" if dt == torch.bfloat16 else "f16",
+                        kv_split=kv_split(dev, B, H, Sq, Skv, D, causal))
+    ref = orc.sdpa_reference(qn, kn, vn, causal=causal, sm_scale=sm)
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS, (err, float(np.abs(emu).max()))
+    assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
+    assert float((got == emu).mean()) >= SAME_BITS[dt]
