@@ -78,3 +78,69 @@ def test_random_shapes_vs_emulation(dev, case):
     assert err <= MAX_ABS, (err, float(np.abs(emu).max()))
     assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
     assert float((got == emu).mean()) >= SAME_BITS[dt]
+
+
+def _mask_cases(n=20, seed=777):
+    rng = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([64, 96, 128, 256]))
+        Hkv = int(rng.randint(1, 3))
+        H = Hkv * int(rng.choice([1, 2]))
+        B = int(rng.randint(1, 3))
+        Skv = int(rng.randint(1, 900))
+        causal = bool(rng.rand() < 0.3)
+        Sq = int(rng.randint(1, min(Skv, 400) + 1)) if causal else int(rng.randint(1, 400))
+        dt = torch.bfloat16 if rng.rand() < 0.6 else torch.float16
+        layout = "HND" if rng.rand() < 0.6 else "NHD"
+        shape = [(Skv,), (1, 1, 1, Skv), (B, 1, 1, Skv), (Sq, Skv), (1, H, Sq, Skv), (B, H, Sq, Skv)][rng.randint(6)]
+        kind = ["bool", "bool", "bool", "float"][rng.randint(4)]
+        p = float(rng.choice([0.3, 0.7, 0.95, 1.0]))
+        out.append((i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, shape, kind, p))
+    return out
+
+
+MASK_CASES = _mask_cases()
+
+
+def _mask_ids(c):
+    i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, shape, kind, p = c
+    return (f"{i}-B{B}H{H}/{Hkv}-{Sq}x{Skv}-d{D}-{'bf16' if dt == torch.bfloat16 else 'f16'}-{layout}"
+            f"{'-causal' if causal else ''}-{kind}{list(shape)}-p{p}")
+
+
+@pytest.mark.parametrize("case", MASK_CASES, ids=[_mask_ids(c) for c in MASK_CASES])
+def test_random_masks_vs_emulation(dev, case):
+    """Random bool masks (density 0.3 to 1, any broadcast shape torch SDPA takes) and additive masks of the inputs'
+    dtype (0 where a bool mask is True, -inf elsewhere, plus a bias of up to +-4 on the visible keys)."""
+    i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, shape, kind, p = case
+    g = torch.Generator().manual_seed(5000 + i)
+    q = torch.randn(B, H, Sq, D, generator=g).to(dt)
+    k = torch.randn(B, Hkv, Skv, D, generator=g).to(dt)
+    v = torch.randn(B, Hkv, Skv, D, generator=g).to(dt)
+    keep = torch.rand(shape, generator=g) < p
+    if kind == "bool":
+        mask = keep
+    else:
+        bias = (torch.rand(shape, generator=g) * 8 - 4)
+        mask = torch.where(keep, bias, torch.full_like(bias, float("-inf"))).to(dt)
+    if layout == "NHD":
+        q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), tensor_layout=layout, is_causal=causal,
+                               attn_mask=mask.to(dev))
+    assert out.shape == q.shape and out.dtype == dt
+    got = hnd_np(out, layout)
+    assert np.isfinite(got).all()
+    qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
+    q8, qs = orc.quant_q(qn)
+    k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(Skv))
+    m = torch.broadcast_to(mask, (B, H, Sq, Skv))
+    m = m.numpy() if kind == "bool" else m.float().numpy()
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, Skv, causal=causal, block_n=32,
+                        out_dtype="bf16" if dt == torch.bfloat16 else "f16",
+                        kv_split=kv_split(dev, B, H, Sq, Skv, D, False), attn_mask=m)
+    ref = orc.sdpa_reference(qn, kn, vn, causal=causal, attn_mask=m)
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS, (err, float(np.abs(emu).max()))
+    assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
+    assert float((got == emu).mean()) >= SAME_BITS[dt]
