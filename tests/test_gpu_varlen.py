@@ -218,3 +218,41 @@ def test_varlen_mixed_lengths_at_scale(dev):
         ms[name] = e0.elapsed_time(e1) / 10
     print(f"varlen 6 sequences (sum {sum(lq)} tokens, 24 heads, d128): packed {ms['packed']:.3f} ms, "
           f"per-sequence calls {ms['per-sequence']:.3f} ms")
+
+
+def _random_varlen_cases(n=12, seed=4242):
+    rng = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        batch = int(rng.randint(1, 7))
+        lk = [int(rng.choice([0, int(rng.randint(1, 70)), int(rng.randint(70, 900))], p=[0.1, 0.3, 0.6]))
+              for _ in range(batch)]
+        causal = bool(rng.rand() < 0.5)
+        lq = [int(rng.choice([0, int(rng.randint(1, 64)), int(rng.randint(64, 700))], p=[0.1, 0.3, 0.6]))
+              for _ in range(batch)]
+        D = int(rng.choice([64, 96, 128, 256]))
+        Hkv = int(rng.randint(1, 3))
+        H = Hkv * int(rng.choice([1, 2, 4]))
+        dt = torch.bfloat16 if rng.rand() < 0.6 else torch.float16
+        out.append((i, lq, lk, H, Hkv, D, dt, causal))
+    return out
+
+
+RANDOM_VARLEN = _random_varlen_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM_VARLEN, ids=[f"{c[0]}-b{len(c[1])}-d{c[5]}-H{c[3]}/{c[4]}"
+                                                      f"{'-causal' if c[7] else ''}" for c in RANDOM_VARLEN])
+def test_varlen_random_batches(dev, case):
+    """Seeded random packed batches (1-6 sequences; empty query sequences, sequences without keys, causal sequences
+    longer than their keys, GQA, head dims 64-256): every sequence a separate call can run is bit-equal to it, and
+    the whole pass is within the emulation's gate."""
+    i, lq, lk, H, Hkv, D, dt, causal = case
+    if sum(lq) == 0 or sum(lk) == 0:
+        lq[0], lk[0] = max(lq[0], 5), max(lk[0], 7)   # the packed totals must be positive
+    q, k, v, cu_q, cu_k = _packed(lq, lk, H, Hkv, D, dt, seed=9000 + i)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    r = _varlen_capi(qd, kd, vd, cu_q, cu_k, causal)
+    assert int(r["ws"][:4].view(torch.int32)[0]) == 0
+    _check_against_separate_calls(qd, kd, vd, cu_q, cu_k, causal, r)
+    _check_against_oracle(q, k, v, cu_q, cu_k, causal, r["out"], "bf16" if dt == torch.bfloat16 else "f16")
