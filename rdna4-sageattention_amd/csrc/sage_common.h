@@ -63,6 +63,17 @@ template <int CTRL> __device__ __forceinline__ double dpp_f64(double x) {
   const int phi = __builtin_amdgcn_mov_dpp(hi, CTRL, 0xF, 0xF, false);
   return __hiloint2double(phi, plo);
 }
+
+// A scheduling fence for the 32 values of a wave's tile (float[2][16]): every value passes through this empty
+// statement, so the instructions producing them issue before it and those consuming them after it.
+#define SAGE_PHASE_FENCE(a)                                                                                \
+  asm volatile("" : "+v"(a[0][0]), "+v"(a[0][1]), "+v"(a[0][2]), "+v"(a[0][3]), "+v"(a[0][4]), "+v"(a[0][5]), \
+                     "+v"(a[0][6]), "+v"(a[0][7]), "+v"(a[0][8]), "+v"(a[0][9]), "+v"(a[0][10]), "+v"(a[0][11]), \
+                     "+v"(a[0][12]), "+v"(a[0][13]), "+v"(a[0][14]), "+v"(a[0][15]), "+v"(a[1][0]), "+v"(a[1][1]), \
+                     "+v"(a[1][2]), "+v"(a[1][3]), "+v"(a[1][4]), "+v"(a[1][5]), "+v"(a[1][6]), "+v"(a[1][7]), \
+                     "+v"(a[1][8]), "+v"(a[1][9]), "+v"(a[1][10]), "+v"(a[1][11]), "+v"(a[1][12]), "+v"(a[1][13]), \
+                     "+v"(a[1][14]), "+v"(a[1][15]))
+
 // Wait until at most N of this wave's vector memory operations are outstanding (they complete in issue order)
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 15, "vmcnt immediate");
