@@ -455,15 +455,16 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       m = slow_ ? m1_ : m2_;                                                                               \
       negm = 0.0f - cl * (m == -INFINITY ? 0.0f : m);                                                      \
     }                                                                                                      \
-    /* p = exp2(arg); each block's fp32 sum starts from its first p (0 + p is p).  All 32 exponent arguments \
-       are formed before the first exponential (SAGE_PHASE_FENCE): interleaved, each v_exp_f32 waits on the    \
-       FMA just before it, which three waves per SIMD do not hide */                                       \
+    /* p = exp2(arg); each block's fp32 sum starts from its first p (0 + p is p).  Up to head dim 128 and   \
+       without a mask all 32 exponent arguments are formed before the first exponential (SAGE_PHASE_FENCE):  \
+       interleaved, each v_exp_f32 waits on the FMA just before it, which three waves per SIMD do not hide.   \
+       The mask variant (three tile bodies) and head dim 256 hold more registers and would spill with it. */ \
     float psum0_, psum1_;                                                                                  \
     _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
       sf_[0][v_] = (MODE) == 3 ? sf_[0][v_] + nk0_ : __builtin_fmaf(sf_[0][v_], ct0_, nk0_);               \
       sf_[1][v_] = (MODE) == 3 ? sf_[1][v_] + nk1_ : __builtin_fmaf(sf_[1][v_], ct1_, nk1_);               \
     }                                                                                                      \
-    SAGE_PHASE_FENCE(sf_);                                                                                 \
+    if constexpr (!MASK && HD <= 128) SAGE_PHASE_FENCE(sf_);                                               \
     _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
       sf_[0][v_] = __builtin_amdgcn_exp2f(sf_[0][v_]);                                                     \
       sf_[1][v_] = __builtin_amdgcn_exp2f(sf_[1][v_]);                                                     \
