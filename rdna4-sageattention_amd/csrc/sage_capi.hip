@@ -34,6 +34,8 @@ int attn_impl(const int8_t*, const float*, const int8_t*, const float*, const ui
               int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*, int64_t, void*);
 int attn_plan_impl(int, int, int, int, int, int, int*, int*, int64_t*);
 int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D);
+int forward_inputs_check(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, const void*,
+                         int64_t, int64_t, int64_t, int, int, int, int, int, int, int, const char*);
 struct MaskPrep;
 int forward_quant_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, const void*,
                        int64_t, int64_t, int64_t, int, int, int, int, int, int, int, float, int8_t*, float*, float*,
@@ -129,7 +131,9 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
   if (!sage::head_dim_ok(D))
     return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: head_dim %d (supported 64, 96, 128, 256)", D);
   if (causal && Sq > Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "sage_forward: causal attention needs q_len <= kv_len");
-  int rc;
+  int rc = sage::forward_inputs_check(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype,
+                                      "sage_forward");
+  if (rc) return rc;
   if (workspace == nullptr) {
     // no workspace: V maxima by atomics (four quantization launches) and every attention tile whole
     if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;

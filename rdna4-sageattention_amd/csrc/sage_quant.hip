@@ -658,6 +658,18 @@ int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D) {
   return (int64_t)B * Hkv * vamax_chunks(Skv) * layout_dim(D) * (int64_t)sizeof(float);
 }
 
+// sage_forward's inputs, checked before its first launch (sizes, dtype, head dim, pointers and strides of q, k, v).
+int forward_inputs_check(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
+                         int64_t ksh, const void* v, int64_t vsb, int64_t vss, int64_t vsh, int B, int H, int Hkv,
+                         int Sq, int Skv, int D, int dtype, const char* who) {
+  int rc = check_common(B, H, Sq, D, dtype, who);
+  if (rc) return rc;
+  if ((rc = check_common(B, Hkv, Skv, D, dtype, who))) return rc;
+  if ((rc = check_strided(q, qsb, qss, qsh, who, "q"))) return rc;
+  if ((rc = check_strided(k, ksb, kss, ksh, who, "k"))) return rc;
+  return check_strided(v, vsb, vss, vsh, who, "v");
+}
+
 // Validation of every argument is done by the caller (sage_forward) through the per-stage checks below.  mp: the
 // mask work of sage_forward_masked (NULL: none), run as extra workgroups of the two launches.
 int forward_quant_impl(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb, int64_t kss,
@@ -665,12 +677,8 @@ int forward_quant_impl(const void* q, int64_t qsb, int64_t qss, int64_t qsh, con
                        int Skv, int D, int dtype, float qs_mul, int8_t* q8, float* qs, float* vpart, int8_t* k8,
                        float* ks, uint8_t* v8t, float* vs, const MaskPrep* mp, void* stream) {
   const char* who = "sage_forward";
-  int rc = check_common(B, H, Sq, D, dtype, who);
+  int rc = forward_inputs_check(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype, who);
   if (rc) return rc;
-  if ((rc = check_common(B, Hkv, Skv, D, dtype, who))) return rc;
-  if ((rc = check_strided(q, qsb, qss, qsh, who, "q"))) return rc;
-  if ((rc = check_strided(k, ksb, kss, ksh, who, "k"))) return rc;
-  if ((rc = check_strided(v, vsb, vss, vsh, who, "v"))) return rc;
   SAGE_REQUIRE(q8 && qs && vpart && k8 && ks && v8t && vs, "%s: an intermediate pointer is NULL", who);
   SAGE_REQUIRE(aligned16(q8) && aligned16(k8) && aligned16(v8t) && aligned16(vpart) && aligned16(vs),
                "%s: q8 / k8 / v8t / vs / workspace must be 16-byte aligned", who);

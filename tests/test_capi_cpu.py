@@ -101,7 +101,18 @@ def test_forward_validates_before_launching_and_python_raises():
     assert rc == _capi.SAGE_ERR_UNSUPPORTED and "causal" in _err()
     with pytest.raises(_capi.SageError, match="head_dim 80"):
         _capi.call("sage_quant_q", P, 0, 128, 0, 1, 1, 64, 80, 0, 1.0, P, P, None)
-    assert isinstance(ctypes.CDLL, type)
+
+
+@pytest.mark.parametrize("bad, what", [("k", "k is not 16-byte aligned"), ("kss", "strides"), ("q", "q is NULL")])
+def test_forward_without_workspace_checks_q_k_v_first(bad, what):
+    # without a workspace sage_forward's first launch takes the V maxima; a bad q or k must be rejected before it
+    # (here, with no GPU, a launch would fail with a HIP error instead of the argument error)
+    lib = _capi.lib()
+    a = dict(q=P, qsb=0, qss=128, qsh=0, k=P, ksb=0, kss=128, ksh=0, v=P, vsb=0, vss=128, vsh=0)
+    a.update({"k": P + 8} if bad == "k" else {"kss": 100} if bad == "kss" else {"q": None})
+    rc = lib.sage_forward(*a.values(), P, 0, 128, 128, 1, 4, 2, 64, 64, 128, 0, 0, 1.0, P, P, P, P, P, P, None, 0, None)
+    assert rc == _capi.SAGE_ERR_INVALID, _err()
+    assert what in _err()
 
 
 def test_varlen_layout_bounds():
