@@ -76,7 +76,8 @@ const char* sage_manifest_json(void);
  * Hadamard-rotate Q over head_dim and quantize to int8 with one scale per token.
  * Replaces the quant_q launch of src/rdna4_sage/_attention.py:125-126 (kernel kernel_build/sage_quant.py:33-48,
  * kernarg "<4Q5i4x2Q", build_kernels.py:36) and folds the sm_scale multiply of _attention.py:130-131:
- * QS = fp32(fp32(s / D) * qs_mul); pass qs_mul = 1.0f for the default scale.
+ * QS = fp32(fp32(s / D) * qs_mul); pass qs_mul = 1.0f for the default scale.  qs_mul must be positive and finite
+ * (SAGE_ERR_INVALID otherwise); the same holds for the qs_mul of every forward entry point.
  * q: [B, Sq, H, D] addressed as q + b*sb + s*ss + h*sh.
  */
 int sage_quant_q(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H, int Sq, int D, int dtype,

@@ -197,8 +197,10 @@ def e4m3_to_f32(bits: np.ndarray) -> np.ndarray:
 # Quantizers
 # ----------------------------------------------------------------------------------------------------------
 def qs_fold_factor(sm_scale, d: int):
-    """None for the default scale, else fp32(sm_scale * sqrt(D)) (src/rdna4_sage/_attention.py:130-131)."""
-    if sm_scale is None or sm_scale <= 0 or math.isclose(sm_scale, d ** -0.5, rel_tol=1e-6):
+    """None for the default scale, else fp32(sm_scale * sqrt(D)) (src/rdna4_sage/_attention.py:130-131).  A scale
+    that is not positive (NaN included) is the default too: the reference's op passes `sm_scale if sm_scale > 0 else
+    None` (src/rdna4_sage/ops.py:10)."""
+    if sm_scale is None or not sm_scale > 0 or math.isclose(sm_scale, d ** -0.5, rel_tol=1e-6):
         return None
     return F32(sm_scale * math.sqrt(d))
 

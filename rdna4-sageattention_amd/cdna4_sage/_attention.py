@@ -79,10 +79,11 @@ def check_supported(q, k, v, layout, is_causal=False):
 
 
 def qs_fold_factor(sm_scale, head_dim: int) -> float:
-    """Multiplier folded into the Q scales: the kernel has 1/sqrt(D) built in (reference: _attention.py:130-131)."""
-    if sm_scale is not None and not math.isclose(sm_scale, head_dim ** -0.5, rel_tol=1e-6):
-        return float(sm_scale * math.sqrt(head_dim))
-    return 1.0
+    """Multiplier folded into the Q scales: the kernel has 1/sqrt(D) built in (reference: _attention.py:130-131).
+    None, a non-positive scale and NaN select the default, as the reference's op does (src/rdna4_sage/ops.py:10)."""
+    if sm_scale is None or not sm_scale > 0 or math.isclose(sm_scale, head_dim ** -0.5, rel_tol=1e-6):
+        return 1.0
+    return float(sm_scale * math.sqrt(head_dim))
 
 
 def _ptr(t: torch.Tensor) -> int:

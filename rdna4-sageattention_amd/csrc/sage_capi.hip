@@ -134,6 +134,7 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
   int rc = sage::forward_inputs_check(q, qsb, qss, qsh, k, ksb, kss, ksh, v, vsb, vss, vsh, B, H, Hkv, Sq, Skv, D, dtype,
                                       "sage_forward");
   if (rc) return rc;
+  if ((rc = sage::check_qs_mul(qs_mul, "sage_forward"))) return rc;
   if (workspace == nullptr) {
     // no workspace: V maxima by atomics (four quantization launches) and every attention tile whole
     if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;
@@ -166,12 +167,13 @@ int sage_forward_noalloc(const void* q, int64_t qsb, int64_t qss, int64_t qsh, c
   SAGE_REQUIRE(H % Hkv == 0, "%s: heads %d not a multiple of kv heads %d", who, H, Hkv);
   if (!sage::head_dim_ok(D)) return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: head_dim %d (supported 64, 96, 128, 256)", who, D);
   if (causal && Sq > Skv) return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: causal attention needs q_len <= kv_len", who);
+  int rc = sage::check_qs_mul(qs_mul, who);
+  if (rc) return rc;
   // the intermediates of sage_forward, then its workspace, each 256-byte aligned
   const int64_t dl = sage::layout_dim(D), skp = sage::kv_pad(Skv);
   const int64_t nq = (int64_t)B * H * Sq, nkv = (int64_t)B * Hkv;
   int64_t attn_bytes = 0, ws_bytes = 0;
-  int rc = sage::forward_workspace(B, H, Hkv, Sq, Skv, D, causal, &attn_bytes, &ws_bytes);
-  if (rc) return rc;
+  if ((rc = sage::forward_workspace(B, H, Hkv, Sq, Skv, D, causal, &attn_bytes, &ws_bytes))) return rc;
   const int64_t o_q8 = 0;
   const int64_t o_qs = o_q8 + sage::align256(nq * dl);
   const int64_t o_k8 = o_qs + sage::align256(nq * 4);

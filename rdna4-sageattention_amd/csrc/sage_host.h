@@ -35,6 +35,14 @@ inline int check_launch(const char* what) {
   return SAGE_OK;
 }
 
+// the factor folded into the Q scales (sm_scale * sqrt(head_dim)): the attention assumes positive, finite row
+// scales (its row maxima are taken on the raw integer scores), so anything else is rejected (NaN fails both tests)
+inline int check_qs_mul(float qs_mul, const char* who) {
+  SAGE_REQUIRE(qs_mul > 0.0f && qs_mul <= 3.402823466e38f, "%s: qs_mul must be positive and finite (got %g)", who,
+               (double)qs_mul);
+  return SAGE_OK;
+}
+
 // head dims of the path, and the channel count of their int8 / E4M3 layouts (96 is stored zero-padded to 128)
 __host__ __device__ constexpr bool head_dim_ok(int d) { return d == 64 || d == 96 || d == 128 || d == 256; }
 __host__ __device__ constexpr int layout_dim(int d) { return d == 96 ? 128 : d; }

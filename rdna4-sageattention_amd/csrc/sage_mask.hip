@@ -127,6 +127,7 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
   if (mask_dtype != SAGE_DTYPE_BOOL && mask_dtype != dtype)
     return sage::fail(SAGE_ERR_UNSUPPORTED, "%s: a float mask must have the inputs' dtype", who);
   SAGE_REQUIRE(mask != nullptr, "%s: mask is NULL", who);
+  if ((rc = sage::check_qs_mul(qs_mul, who))) return rc;
   SAGE_REQUIRE(out != nullptr && sage::aligned16(out), "%s: out must be non-NULL and 16-byte aligned", who);
   SAGE_REQUIRE(osb % 8 == 0 && oss % 8 == 0 && osh % 8 == 0 && osb >= 0 && oss >= 0 && osh >= 0,
                "%s: out strides must be non-negative multiples of 8 elements", who);

@@ -621,6 +621,7 @@ int quant_q_impl(const void* q, int64_t sb, int64_t ss, int64_t sh, int B, int H
   const char* who = "sage_quant_q";
   int rc = check_common(B, H, Sq, D, dtype, who);
   if (rc) return rc;
+  if ((rc = check_qs_mul(qs_mul, who))) return rc;
   if ((rc = check_strided(q, sb, ss, sh, who, "q"))) return rc;
   SAGE_REQUIRE(q8 != nullptr && qs != nullptr, "%s: q8 / qs is NULL", who);
   SAGE_REQUIRE(aligned16(q8), "%s: q8 is not 16-byte aligned", who);

@@ -265,6 +265,7 @@ int sage_forward_varlen(const void* q, int64_t qss, int64_t qsh, const void* k, 
   if ((rc = sage::check_packed(k, kss, ksh, "k"))) return rc;
   if ((rc = sage::check_packed(v, vss, vsh, "v"))) return rc;
   if ((rc = sage::check_packed(out, oss, osh, "out"))) return rc;
+  if ((rc = sage::check_qs_mul(qs_mul, "sage_forward_varlen"))) return rc;
   SAGE_REQUIRE(cu_seqlens_q && cu_seqlens_k, "sage_forward_varlen: cu_seqlens is NULL");
   SAGE_REQUIRE(q8 && qs && k8 && ks && v8t && vs, "sage_forward_varlen: an intermediate pointer is NULL");
   SAGE_REQUIRE(sage::aligned16(q8) && sage::aligned16(k8) && sage::aligned16(v8t) && sage::aligned16(vs),

@@ -288,3 +288,16 @@ def test_lse_with_non_positive_sm_scale_uses_it_as_given():
         lse = sageattention.core._lse(q, k, "HND", False, sm)
         s = torch.matmul(q.double(), k.double().transpose(-1, -2)) * sm
         torch.testing.assert_close(lse.double(), torch.logsumexp(s, -1), atol=2e-3, rtol=1e-4)
+
+
+def test_qs_fold_factor_maps_non_positive_scales_to_the_default():
+    """The attention's scale fold (the dense, masked and packed varlen passes all use it): None, the default 1/sqrt(D),
+    0, negative values and NaN fold nothing, as the reference's op maps sm_scale <= 0 to None
+    (src/rdna4_sage/ops.py:10); any other positive scale folds sm_scale * sqrt(D), as the oracle does."""
+    from cdna4_sage._attention import qs_fold_factor
+    for sm in (None, 128 ** -0.5, 0.0, -0.25, float("nan")):
+        assert qs_fold_factor(sm, 128) == 1.0
+        assert orc.qs_fold_factor(sm, 128) is None
+    for sm, d in ((0.05, 128), (0.3, 64), (1.0, 96)):
+        assert qs_fold_factor(sm, d) == pytest.approx(sm * d ** 0.5, rel=1e-12)
+        assert np.float32(qs_fold_factor(sm, d)) == orc.qs_fold_factor(sm, d)

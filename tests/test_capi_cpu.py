@@ -103,6 +103,20 @@ def test_forward_validates_before_launching_and_python_raises():
         _capi.call("sage_quant_q", P, 0, 128, 0, 1, 1, 64, 80, 0, 1.0, P, P, None)
 
 
+@pytest.mark.parametrize("qs_mul", [0.0, -1.0, float("nan"), float("inf")])
+def test_qs_mul_must_be_positive_and_finite(qs_mul):
+    # the attention takes its row maxima on the raw integer scores, which needs positive row scales
+    lib = _capi.lib()
+    assert lib.sage_quant_q(P, 0, 128, 0, 1, 1, 64, 128, 0, qs_mul, P, P, None) == _capi.SAGE_ERR_INVALID
+    assert "qs_mul" in _err()
+    rc = lib.sage_forward(P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128, 1, 4, 2, 64, 64, 128, 0, 0, qs_mul,
+                          P, P, P, P, P, P, None, 0, None)
+    assert rc == _capi.SAGE_ERR_INVALID and "qs_mul" in _err()
+    rc = lib.sage_forward_noalloc(P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 128, 1, 4, 2, 64, 64, 128, 0, 0,
+                                  qs_mul, None)
+    assert rc == _capi.SAGE_ERR_INVALID and "qs_mul" in _err()
+
+
 @pytest.mark.parametrize("bad, what", [("k", "k is not 16-byte aligned"), ("kss", "strides"), ("q", "q is NULL")])
 def test_forward_without_workspace_checks_q_k_v_first(bad, what):
     # without a workspace sage_forward's first launch takes the V maxima; a bad q or k must be rejected before it
@@ -161,6 +175,7 @@ def test_varlen_validates_before_launching():
     assert call(v8t=None) == _capi.SAGE_ERR_INVALID
     assert call(ws_bytes=ws_bytes - 1) == _capi.SAGE_ERR_INVALID and "workspace" in _err()
     assert call(ws=P + 16) == _capi.SAGE_ERR_INVALID and "256-byte" in _err()
+    assert call(qs_mul=float("nan")) == _capi.SAGE_ERR_INVALID and "qs_mul" in _err()
     assert call(total_q=0) == _capi.SAGE_ERR_INVALID
 
 
@@ -187,6 +202,7 @@ def test_masked_forward_validates_before_launching():
     assert call(oss=100) == _capi.SAGE_ERR_INVALID and "multiples of 8" in _err()
     assert call(ws=None) == _capi.SAGE_ERR_INVALID and "workspace" in _err()
     assert call(ws=P + 16) == _capi.SAGE_ERR_INVALID and "256-byte" in _err()
+    assert call(qs_mul=-0.5) == _capi.SAGE_ERR_INVALID and "qs_mul" in _err()
     assert call(Sq=1 << 20, Skv=1 << 30) == _capi.SAGE_ERR_INVALID and "too large" in _err()
     assert call(mask_dtype=7) == _capi.SAGE_ERR_UNSUPPORTED and "mask dtype" in _err()
     assert call(mask_dtype=_capi.DTYPE_F16) == _capi.SAGE_ERR_UNSUPPORTED and "inputs' dtype" in _err()

@@ -181,6 +181,11 @@ def test_varlen_python_api_and_router(dev):
     v0 = vd[:1500].float().repeat_interleave(4, 1).transpose(0, 1).contiguous()       # [8, 1500, 128]
     ref = torch.softmax(torch.matmul(q0, kt) * 0.05, dim=-1).matmul(v0)
     assert cosine(o2[:1500].float().cpu().numpy(), ref.transpose(0, 1).cpu().numpy()) >= COS
+    # a scale that is not positive selects the default 1/sqrt(D), as the reference's op does for its per-sequence calls
+    # (it used to fold into the Q scales as 0 or a negative factor)
+    for sm in (0.0, -0.05, float("nan")):
+        o3 = cdna4_sage.attention_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), sm_scale=sm, is_causal=True)
+        assert torch.equal(o3[:4300], out[:4300])
     # all sequences shorter than the kernel's minimum key length: the reference's per-sequence routing (SDPA here)
     q, k, v, cu_q, cu_k = _packed([100, 300], [200, 300], 4, 4, 64, torch.bfloat16, seed=12)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
