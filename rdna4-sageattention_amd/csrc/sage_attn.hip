@@ -175,16 +175,20 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     kofs = vt.kp[b];
     obase = out + (int64_t)qb * oss;
   } else {
-    int logical;
-    if (!split) {
-      logical = xcd_remap(blockIdx.x, n_full);
+    int bh;
+    if (CAUSAL) {
+      causal_tile(blockIdx.x, total / q_tiles, q_tiles, bh, qt);  // causal launches are never split
     } else {
-      unit = blockIdx.x - n_full;
-      logical = n_full + unit / chunks;
+      int logical;
+      if (!split) {
+        logical = xcd_remap(blockIdx.x, n_full);
+      } else {
+        unit = blockIdx.x - n_full;
+        logical = n_full + unit / chunks;
+      }
+      bh = logical / q_tiles;
+      qt = logical % q_tiles;
     }
-    const int bh = logical / q_tiles;
-    qt = logical % q_tiles;
-    if (CAUSAL) qt = q_tiles - 1 - qt;  // longest rows first within a head
     b = bh / H;
     h = bh % H;
     qrow0 = (int64_t)bh * Sq;

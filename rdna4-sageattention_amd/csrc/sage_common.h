@@ -213,4 +213,22 @@ __device__ __forceinline__ int xcd_remap(int id, int total) {
   return x * q + (x < r ? x : r) + i;
 }
 
+// Causal launches (tiles of different lengths): the (batch, head) pair and query tile of workgroup `id` among
+// bh_count * q_tiles.  When the pairs divide over the 8 XCDs, XCD x keeps its own group of pairs (nh of them: their K/V
+// stays in its L2) and takes their tiles longest first across the group: the last query tile of every pair, then the
+// one before, and so on, so that every pair's short tiles come last.  Otherwise: each XCD a contiguous range, longest
+// first within each pair.
+__device__ __forceinline__ void causal_tile(int id, int bh_count, int q_tiles, int& bh, int& qt) {
+  constexpr int NX = 8;
+  if (bh_count % NX == 0) {
+    const int nh = bh_count / NX, x = id % NX, i = id / NX;
+    bh = x * nh + i % nh;
+    qt = q_tiles - 1 - i / nh;
+  } else {
+    const int logical = xcd_remap(id, bh_count * q_tiles);
+    bh = logical / q_tiles;
+    qt = q_tiles - 1 - logical % q_tiles;
+  }
+}
+
 }  // namespace sage

@@ -56,10 +56,14 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
   constexpr int LOADS = KTILE / 1024 / 4;  // 1 KiB direct loads per wave per tile
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][KTILE];
 
-  const int logical = xcd_remap(blockIdx.x, total);
-  const int bh = logical / q_tiles;
-  int qt = logical % q_tiles;
-  if (CAUSAL) qt = q_tiles - 1 - qt;  // longest rows first within a head
+  int bh, qt;
+  if (CAUSAL) {
+    causal_tile(blockIdx.x, total / q_tiles, q_tiles, bh, qt);
+  } else {
+    const int logical = xcd_remap(blockIdx.x, total);
+    bh = logical / q_tiles;
+    qt = logical % q_tiles;
+  }
   const int b = bh / H, h = bh % H;
   const int hkv = h / (H / Hkv);
   const int tid = threadIdx.x;
