@@ -181,8 +181,8 @@ __global__ __launch_bounds__(VL_META_THREADS) void varlen_meta_kernel(const int*
 // grid-stride over max(n_tiles, n_kblk, n_vs)
 __global__ __launch_bounds__(256) void varlen_prep_kernel(const int* __restrict__ hdr, const int* __restrict__ cu_q,
                                                           const int* __restrict__ kp, const int* __restrict__ order,
-                                                          const int* __restrict__ tpre, int batch, int causal,
-                                                          int n_tiles, int n_kblk, int4* __restrict__ tiles,
+                                                          const int* __restrict__ tpre, int batch, int H,
+                                                          int causal, int n_tiles, int n_kblk, int4* __restrict__ tiles,
                                                           int* __restrict__ ktab, float* __restrict__ vs,
                                                           int64_t n_vs) {
   const int T = hdr[1], kp_total = hdr[2];
@@ -201,9 +201,9 @@ __global__ __launch_bounds__(256) void varlen_prep_kernel(const int* __restrict_
         const int b = order[lo];
         const int r = (int)i - tpre[lo];
         const int nq = (cu_q[b + 1] - cu_q[b] + 127) / 128;
-        int qt = r % nq;
-        if (causal) qt = nq - 1 - qt;  // longest rows first
-        e = make_int4(b, r / nq, qt, 0);
+        // causal: the sequence's tiles longest first across its heads (its last query tile of every head, then the one
+        // before, ...), so that its short tiles come last; otherwise head by head
+        e = causal ? make_int4(b, r % H, nq - 1 - r / H, 0) : make_int4(b, r / nq, r % nq, 0);
       }
       tiles[i] = e;
     }
@@ -291,7 +291,7 @@ int sage_forward_varlen(const void* q, int64_t qss, int64_t qsh, const void* k, 
   const int64_t n_items = std::max<int64_t>(std::max(L.n_blocks, n_kblk), n_vs);
   const int grid = (int)std::min<int64_t>((n_items + 255) / 256, 4096);
   hipLaunchKernelGGL(sage::varlen_prep_kernel, dim3(grid), dim3(256), 0, st, hdr, cu_seqlens_q, kp, order, tpre, batch,
-                     causal ? 1 : 0, L.n_blocks, n_kblk, tiles, ktab, vs, n_vs);
+                     H, causal ? 1 : 0, L.n_blocks, n_kblk, tiles, ktab, vs, n_vs);
   if ((rc = sage::check_launch("varlen prep launch"))) return rc;
   if ((rc = sage::varlen_quant_impl(q, qss, qsh, k, kss, ksh, v, vss, vsh, H, Hkv, total_q, L.tkp, D, dtype, qs_mul,
                                     cu_seqlens_k, kp, ktab, q8, qs, k8, ks, v8t, vs, stream)))
