@@ -1,5 +1,7 @@
 """gfx950 LSE kernel (the row logsumexp `return_lse` returns) vs float64 on the CPU oracle and vs the reference's own
 gate: atol 2e-3, rtol 1e-4 against fp32 torch (tests/test_sageattention.py:70 of the reference)."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -112,3 +114,38 @@ def test_return_lse_with_non_positive_sm_scale_uses_it_as_given(dev):
         torch.testing.assert_close(lse.cpu().double(), torch.logsumexp(s, -1), atol=2e-3, rtol=1e-4)
     _, lse0 = sageattention.sageattn(qd, kd, kd, tensor_layout="HND", sm_scale=0.0, return_lse=True)
     torch.testing.assert_close(lse0.cpu(), torch.full((1, 2, 300), float(np.log(1100.0))), atol=1e-4, rtol=0)
+
+
+def _random_lse_cases(n=16, seed=4242):
+    """Seeded random LSE shapes within the kernel's domain (D 64 or 128, causal only with q_len <= kv_len)."""
+    rng = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([64, 128]))
+        Hkv = int(rng.randint(1, 4))
+        H = Hkv * int(rng.choice([1, 2, 4]))
+        B = int(rng.randint(1, 3))
+        Skv = int(rng.choice([int(rng.randint(1, 130)), int(rng.randint(130, 1500))]))
+        causal = bool(rng.rand() < 0.5)
+        Sq = int(rng.randint(1, Skv + 1)) if causal else int(rng.randint(1, 700))
+        dt = torch.bfloat16 if rng.rand() < 0.6 else torch.float16
+        layout = "HND" if rng.rand() < 0.6 else "NHD"
+        sm = None if rng.rand() < 0.7 else float(rng.uniform(0.03, 0.2))
+        out.append((i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, sm))
+    return out
+
+
+RANDOM_LSE = _random_lse_cases(seed=4242 + int(os.environ.get("SAGE_SWEEP_SEED", "0")))
+
+
+@pytest.mark.parametrize("case", RANDOM_LSE, ids=[
+    f"{c[0]}-B{c[1]}H{c[2]}/{c[3]}-{c[4]}x{c[5]}-d{c[6]}-{c[8]}{'-causal' if c[9] else ''}{'-sm' if c[10] else ''}"
+    for c in RANDOM_LSE])
+def test_random_lse_vs_float64(dev, case):
+    """Random shapes, GQA groups, layouts and scales against the float64 logsumexp, at the bound of the fixed cases."""
+    i, B, H, Hkv, Sq, Skv, D, dt, layout, causal, sm = case
+    q, k = _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=1000 + i)
+    got = cdna4_sage.lse(q.to(dev), k.to(dev), layout, sm, causal).cpu().numpy()
+    assert got.shape == (B, H, Sq) and np.isfinite(got).all()
+    ref = orc.lse_reference(_hnd(q, layout), _hnd(k, layout), causal=causal, sm_scale=sm)
+    assert np.abs(got - ref).max() <= 1e-4 + 1e-6 * np.abs(ref).max()
