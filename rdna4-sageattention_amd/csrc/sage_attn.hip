@@ -147,6 +147,12 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   constexpr uint32_t SEED_BITS = SEEDED ? 0x3E22F983u : 0u;
   constexpr float SEED_F = __builtin_bit_cast(float, SEED_BITS);
   constexpr float SSCALE = SEEDED ? 67108864.0f : 1.0f;  // 2^26
+  // Passes of a tile body: speculative (the offsets of the current m, no block maxima), exact (the block maxima and
+  // the reference's rescale decisions), and the redo of block 1 after a block-1 rescale.  The mask variant and head
+  // dim 256 (which would spill with the speculative code) have no speculative pass.
+  constexpr int PASS_NONE = 0, PASS_SPEC = 1, PASS_EXACT = 2, PASS_REDO = 3;
+  constexpr bool SPEC_OK = !MASK && HD <= 128;
+  constexpr float SPEC_SUM = 181.0f;  // below 2^7.5: a margin of 2^0.5 under the threshold for fp32 rounding
   // K / V tile buffers: three where they fit (the unmasked loops prefetch two tiles ahead, which hides the direct
   // loads' latency behind two tiles of arithmetic), two for head dim 256 (3 x 32 KiB per workgroup would leave room
   // for one workgroup per CU) and for the mask variant (whose loops prefetch one tile ahead)
@@ -304,6 +310,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
   float m = -INFINITY, l = 0.0f;
   float negm = 0.0f;  // -(cl * m_ref), m_ref = m or 0 while m = -inf: the exponent offset while m stays
+  bool fastok = false;  // every lane of the wave has a finite m: its tiles start with a speculative pass
   v8i pb = {};  // E4M3 probabilities (B operand of the PV MFMA); each cvt rewrites one half, so no clearing
   v4i bw_none[4] = {};  // the bias argument of the tile bodies without an additive mask (never read)
 
@@ -314,17 +321,21 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   // masked (MW = the lane's mask word of the tile); 3: the additive mask values BW (the lane's 32 16-bit values,
   // input dtype, -inf = masked) added in log2 units, with the row max taken over the biased logits.
   // The rescale decision is taken once per 32-key block, as the reference's 32-key tiles take it
-  // (kernel_build/make_sage_r2.py:180-190): block 0 against m, block 1 against the max m1 that block 0 left.  A
-  // wave-uniform test first asks whether any lane's larger block max moves its max at all; almost always none does,
-  // and then m, the exponent offset negm and l's scale stay as they are (no per-block work).  Otherwise the per-block
-  // decisions run.  When no lane moves its max at block 1, one K = 64 PV MFMA per channel block adds both blocks (the
-  // reference's two PV steps up to the fp32 summation order).  When some lane does (rare: a row's max rising by 2^8
-  // inside a tile), the wave runs the tile body twice before the tile's barrier: pass 0 adds block 0 alone (block 1's
-  // exponent offset is -inf, so its probabilities, sum and E4M3 bytes are 0, and m = m1), pass 1 (REDO) masks block 0
-  // and adds block 1, whose rescale then comes before its MFMA.  No MFMA sits in a branch: around one the compiler
+  // (kernel_build/make_sage_r2.py:180-190): block 0 against m, block 1 against the max m1 that block 0 left.  Once
+  // every lane of the wave has a finite m, a tile starts with a speculative pass (PASS_SPEC) that takes no block
+  // maxima: it forms the probabilities with the current m and stands when every lane's sums are small enough that
+  // no row's max can have moved (almost every tile); otherwise it adds nothing and the tile runs an exact pass.  In
+  // an exact pass (PASS_EXACT) a wave-uniform test first asks whether any lane's larger block max moves its max at
+  // all; if none does, m, the exponent offset negm and l's scale stay as they are (no per-block work).  Otherwise the
+  // per-block decisions run.  When no lane moves its max at block 1, one K = 64 PV MFMA per channel block adds both
+  // blocks (the reference's two PV steps up to the fp32 summation order).  When some lane does (rare: a row's max
+  // rising by 2^8 inside a tile), the wave runs the tile body again before the tile's barrier: the exact pass adds
+  // block 0 alone (block 1's exponent offset is -inf, so its probabilities, sum and E4M3 bytes are 0, and m = m1),
+  // the redo pass (PASS_REDO) masks block 0 and adds block 1, whose rescale then comes before its MFMA.  No MFMA
+  // sits in a branch: around one the compiler
   // loses the accumulators' coalescing and spills the whole loop; the O rescale sits in its own branch after the
   // exponentials for the same reason.
-#define SAGE_TILE(T, MODE, MW, BW, REDO)                                                                       \
+#define SAGE_TILE(T, MODE, MW, BW, KIND)                                                                       \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
     const uint8_t* kt_ = smem[t_ % NBUF];                                                                  \
@@ -360,104 +371,108 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           sf_[kb_][v_] = __int_as_float((__float_as_int(sf_[kb_][v_]) & keep_) | (int)(0xFF800000u & ~(uint32_t)keep_)); \
         }                                                                                                  \
     }                                                                                                      \
-    if (REDO) {                                                                                            \
+    if ((KIND) == PASS_REDO) {                                                                             \
       _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[0][v_] = -INFINITY;                            \
     }                                                                                                      \
     const float ks0_ = ksb[2 * t_], ks1_ = ksb[2 * t_ + 1];                                                \
     const float ct0_ = cl * ks0_, ct1_ = cl * ks1_;                                                        \
-    /* the two 32-key blocks' row maxima, one per lane half (block hf's, for row ln): MODE 3 in log2 units of the \
-       biased logits t (kept in sf_), else in m's units, fp32(max S * ks) (scaled by 2^-26 when seeded: mx - c is \
-       exact).  One lane exchange gives block 0's max in lanes 0-31 and block 1's in lanes 32-63. */       \
-    float bmh_;                                                                                            \
-    if ((MODE) == 3) {                                                                                     \
-      /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))) (b = -inf for a masked key gives -inf); the lazy     \
-         rescale compares a block's max of t with m * cl and keeps m in S * ks units (m_new = m_cand / cl) */ \
-      const float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;      \
-      float tm0_ = -INFINITY, tm1_ = -INFINITY;                                                            \
-      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
-        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                \
-          const uint32_t bw_ = (BW)[(16 * kb_ + v_) >> 3][((16 * kb_ + v_) >> 1) & 3];                     \
-          const float b_ = mask_half_to_f32<OUT_DT>((v_ & 1) ? (bw_ >> 16) : (bw_ & 0xFFFFu));             \
-          const float in_ = __builtin_fmaf(b_, 1.44269504088896341f, kb_ ? ns1_ : ns0_);                   \
-          sf_[kb_][v_] = __builtin_fmaf(sf_[kb_][v_], kb_ ? ct1_ : ct0_, in_);                             \
-          if (kb_) tm1_ = fmaxf(tm1_, sf_[kb_][v_]);                                                       \
-          else tm0_ = fmaxf(tm0_, sf_[kb_][v_]);                                                           \
-        }                                                                                                  \
-      bmh_ = halves_max_f32(tm0_, tm1_);                                                                   \
-    } else {                                                                                               \
-      float mxh_;                                                                                          \
-      if (SEEDED) {                                                                                        \
-        /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose \
-           int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */       \
-        int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                            \
-        _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                \
-          mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                    \
-          mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                    \
-        }                                                                                                  \
-        mxh_ = __int_as_float(halves_max_i32(mi0_, mi1_));                                                 \
-      } else {                                                                                             \
-        float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                          \
-        _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                                \
-          mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                  \
-          mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                  \
-        }                                                                                                  \
-        mxh_ = halves_max_f32(mx0_, mx1_);                                                                 \
-      }                                                                                                    \
-      const float ksh_ = hf ? ks1_ : ks0_;                                                                 \
-      bmh_ = SEEDED ? (mxh_ - SEED_F) * ksh_ : mxh_ * ksh_;                                                \
-    }                                                                                                      \
-    /* Does some lane of the wave move its max at either block?  The ballot over both lane halves covers both \
-       blocks of every row (an -inf max against m = -inf gives NaN, false, as the per-block test does).  Then \
-       m stays, and so does the exponent offset negm = -(cl * m_ref). */                                   \
-    const bool any_ = __ballot((MODE) == 3 ? (bmh_ - m * cl) > 8.0f : (bmh_ - m) * cl > 8.0f) != 0;        \
-    float nk0_, nk1_;       /* the blocks' exponent offsets (MODE 3: added to t) */                        \
+    /* the blocks' exponent offsets (MODE 3: added to t) while m stays: -(cl * m_ref) - fp32(c * ct) (seeded), \
+       -(cl * m_ref) (unseeded, and MODE 3 whose t holds the seed term) */                                 \
+    float nk0_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct0_ : negm;                                    \
+    float nk1_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct1_ : negm;                                    \
     float corr_ = 1.0f;     /* the rescale before this pass's MFMA */                                      \
     bool slow_ = false;     /* some lane moves its max at block 1 in a first pass: block 1 waits for pass 1 */ \
     bool resc_ = false;     /* some lane rescales O before this pass's MFMA */                             \
-    if (!any_) {                                                                                           \
-      nk0_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct0_ : negm;                                        \
-      nk1_ = ((MODE) != 3 && SEEDED) ? negm - SEED_F * ct1_ : negm;                                        \
-    } else {                                                                                               \
-      /* the reference's decisions, block 0 against m, block 1 against the max m1 block 0 left */          \
-      float bm0_, bm1_;                                                                                    \
-      halves_split_f32(bmh_, bm0_, bm1_);                                                                  \
-      bool need0_, need1_;                                                                                 \
-      float m1_, m2_;                                                                                      \
+    const bool spec_ = SPEC_OK && (KIND) == PASS_SPEC;                                                     \
+    if (!spec_) {                                                                                          \
+      /* the two 32-key blocks' row maxima, one per lane half (block hf's, for row ln): MODE 3 in log2 units of the \
+         biased logits t (kept in sf_), else in m's units, fp32(max S * ks) (scaled by 2^-26 when seeded: mx - c is \
+         exact).  One lane exchange gives block 0's max in lanes 0-31 and block 1's in lanes 32-63. */     \
+      float bmh_;                                                                                          \
       if ((MODE) == 3) {                                                                                   \
-        const float mc0_ = m * cl;                                                                         \
-        const float mcand0_ = fmaxf(mc0_, bm0_);                                                           \
-        need0_ = (mcand0_ - mc0_) > 8.0f;                                                                  \
-        m1_ = need0_ ? mcand0_ * rcl : m;                                                                  \
-        const float mc1_ = m1_ * cl;                                                                       \
-        const float mcand1_ = fmaxf(mc1_, bm1_);                                                           \
-        need1_ = (mcand1_ - mc1_) > 8.0f;                                                                  \
-        m2_ = need1_ ? mcand1_ * rcl : m1_;                                                                \
+        /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))) (b = -inf for a masked key gives -inf); the lazy   \
+           rescale compares a block's max of t with m * cl and keeps m in S * ks units (m_new = m_cand / cl) */ \
+        const float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;    \
+        float tm0_ = -INFINITY, tm1_ = -INFINITY;                                                          \
+        _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                \
+          _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                              \
+            const uint32_t bw_ = (BW)[(16 * kb_ + v_) >> 3][((16 * kb_ + v_) >> 1) & 3];                   \
+            const float b_ = mask_half_to_f32<OUT_DT>((v_ & 1) ? (bw_ >> 16) : (bw_ & 0xFFFFu));           \
+            const float in_ = __builtin_fmaf(b_, 1.44269504088896341f, kb_ ? ns1_ : ns0_);                 \
+            sf_[kb_][v_] = __builtin_fmaf(sf_[kb_][v_], kb_ ? ct1_ : ct0_, in_);                           \
+            if (kb_) tm1_ = fmaxf(tm1_, sf_[kb_][v_]);                                                     \
+            else tm0_ = fmaxf(tm0_, sf_[kb_][v_]);                                                         \
+          }                                                                                                \
+        bmh_ = halves_max_f32(tm0_, tm1_);                                                                 \
       } else {                                                                                             \
-        const float mcand0_ = fmaxf(m, bm0_);                                                              \
-        need0_ = (mcand0_ - m) * cl > 8.0f;                                                                \
-        m1_ = need0_ ? mcand0_ : m;                                                                        \
-        const float mcand1_ = fmaxf(m1_, bm1_);                                                            \
-        need1_ = (mcand1_ - m1_) * cl > 8.0f;                                                              \
-        m2_ = need1_ ? mcand1_ : m1_;                                                                      \
+        float mxh_;                                                                                        \
+        if (SEEDED) {                                                                                      \
+          /* block maxima on the bit patterns: the scores are positive floats (c + S * 2^-26) or -inf, whose \
+             int32 patterns order like the floats, and an integer max needs no NaN canonicalisation */     \
+          int mi0_ = __float_as_int(sf_[0][0]), mi1_ = __float_as_int(sf_[1][0]);                          \
+          _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                              \
+            mi0_ = max(mi0_, __float_as_int(sf_[0][v_]));                                                  \
+            mi1_ = max(mi1_, __float_as_int(sf_[1][v_]));                                                  \
+          }                                                                                                \
+          mxh_ = __int_as_float(halves_max_i32(mi0_, mi1_));                                               \
+        } else {                                                                                           \
+          float mx0_ = sf_[0][0], mx1_ = sf_[1][0];                                                        \
+          _Pragma("unroll") for (int v_ = 1; v_ < 16; ++v_) {                                              \
+            mx0_ = fmaxf(mx0_, sf_[0][v_]);                                                                \
+            mx1_ = fmaxf(mx1_, sf_[1][v_]);                                                                \
+          }                                                                                                \
+          mxh_ = halves_max_f32(mx0_, mx1_);                                                               \
+        }                                                                                                  \
+        const float ksh_ = hf ? ks1_ : ks0_;                                                               \
+        bmh_ = SEEDED ? (mxh_ - SEED_F) * ksh_ : mxh_ * ksh_;                                              \
       }                                                                                                    \
-      /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets  \
-         from 0 instead of -inf keep corr and the exponents free of NaN */                                 \
-      const float mref1_ = m1_ == -INFINITY ? 0.0f : m1_;                                                  \
-      const float mref2_ = m2_ == -INFINITY ? 0.0f : m2_;                                                  \
-      slow_ = !(REDO) && __ballot(need1_) != 0;                                                            \
-      /* nk = -(cl * m_new) - fp32(c * ct) (seeded), -(cl * m_new) (unseeded, and MODE 3 whose t holds the   \
-         seed term); in a slow first pass block 1's offset is -inf, so its p, sum and E4M3 bytes are 0 */    \
-      const float neg1_ = 0.0f - cl * mref1_, neg2_ = 0.0f - cl * mref2_;                                  \
-      nk0_ = ((MODE) != 3 && SEEDED) ? neg1_ - SEED_F * ct0_ : neg1_;                                      \
-      nk1_ = slow_ ? -INFINITY : (((MODE) != 3 && SEEDED) ? neg2_ - SEED_F * ct1_ : neg2_);                \
-      /* exp2(carg0 + carg1) with carg1 counted unless slow; one of the two is 0 wherever a row has seen a   \
-         key (a non-slow first pass has no block-1 rescale, a redo pass's masked block 0 none at block 0), so \
-         this is the reference's corr0 or corr1; 1 in a lane whose max does not move */                      \
-      const float carg0_ = (m - mref1_) * cl, carg1_ = (m1_ - mref2_) * cl;                                \
-      resc_ = __ballot(need0_ || (!slow_ && need1_)) != 0;                                                 \
-      if (resc_) corr_ = __builtin_amdgcn_exp2f(carg0_ + (slow_ ? 0.0f : carg1_));                         \
-      m = slow_ ? m1_ : m2_;                                                                               \
-      negm = 0.0f - cl * (m == -INFINITY ? 0.0f : m);                                                      \
+      /* Does some lane of the wave move its max at either block?  The ballot over both lane halves covers both \
+         blocks of every row (an -inf max against m = -inf gives NaN, false, as the per-block test does).  Then \
+         m stays, and so does the exponent offset negm = -(cl * m_ref). */                                 \
+      const bool any_ = __ballot((MODE) == 3 ? (bmh_ - m * cl) > 8.0f : (bmh_ - m) * cl > 8.0f) != 0;      \
+      if (any_) {                                                                                          \
+        /* the reference's decisions, block 0 against m, block 1 against the max m1 block 0 left */        \
+        float bm0_, bm1_;                                                                                  \
+        halves_split_f32(bmh_, bm0_, bm1_);                                                                \
+        bool need0_, need1_;                                                                               \
+        float m1_, m2_;                                                                                    \
+        if ((MODE) == 3) {                                                                                 \
+          const float mc0_ = m * cl;                                                                       \
+          const float mcand0_ = fmaxf(mc0_, bm0_);                                                         \
+          need0_ = (mcand0_ - mc0_) > 8.0f;                                                                \
+          m1_ = need0_ ? mcand0_ * rcl : m;                                                                \
+          const float mc1_ = m1_ * cl;                                                                     \
+          const float mcand1_ = fmaxf(mc1_, bm1_);                                                         \
+          need1_ = (mcand1_ - mc1_) > 8.0f;                                                                \
+          m2_ = need1_ ? mcand1_ * rcl : m1_;                                                              \
+        } else {                                                                                           \
+          const float mcand0_ = fmaxf(m, bm0_);                                                            \
+          need0_ = (mcand0_ - m) * cl > 8.0f;                                                              \
+          m1_ = need0_ ? mcand0_ : m;                                                                      \
+          const float mcand1_ = fmaxf(m1_, bm1_);                                                          \
+          need1_ = (mcand1_ - m1_) * cl > 8.0f;                                                            \
+          m2_ = need1_ ? mcand1_ : m1_;                                                                    \
+        }                                                                                                  \
+        /* a row that has seen no key yet (possible only in masked tiles) keeps m = -inf and p = 0: offsets \
+           from 0 instead of -inf keep corr and the exponents free of NaN */                               \
+        const float mref1_ = m1_ == -INFINITY ? 0.0f : m1_;                                                \
+        const float mref2_ = m2_ == -INFINITY ? 0.0f : m2_;                                                \
+        slow_ = (KIND) != PASS_REDO && __ballot(need1_) != 0;                                              \
+        /* nk = -(cl * m_new) - fp32(c * ct) (seeded), -(cl * m_new) (unseeded, and MODE 3 whose t holds the \
+           seed term); in a slow first pass block 1's offset is -inf, so its p, sum and E4M3 bytes are 0 */ \
+        const float neg1_ = 0.0f - cl * mref1_, neg2_ = 0.0f - cl * mref2_;                                \
+        nk0_ = ((MODE) != 3 && SEEDED) ? neg1_ - SEED_F * ct0_ : neg1_;                                    \
+        nk1_ = slow_ ? -INFINITY : (((MODE) != 3 && SEEDED) ? neg2_ - SEED_F * ct1_ : neg2_);              \
+        /* exp2(carg0 + carg1) with carg1 counted unless slow; one of the two is 0 wherever a row has seen a \
+           key (a non-slow first pass has no block-1 rescale, a redo pass's masked block 0 none at block 0), so \
+           this is the reference's corr0 or corr1; 1 in a lane whose max does not move */                  \
+        const float carg0_ = (m - mref1_) * cl, carg1_ = (m1_ - mref2_) * cl;                              \
+        resc_ = __ballot(need0_ || (!slow_ && need1_)) != 0;                                               \
+        if (resc_) corr_ = __builtin_amdgcn_exp2f(carg0_ + (slow_ ? 0.0f : carg1_));                       \
+        m = slow_ ? m1_ : m2_;                                                                             \
+        negm = 0.0f - cl * (m == -INFINITY ? 0.0f : m);                                                    \
+      }                                                                                                    \
+      if (SPEC_OK) fastok = __ballot(m == -INFINITY) == 0;                                                 \
     }                                                                                                      \
     /* p = exp2(arg); each block's fp32 sum starts from its first p (0 + p is p).  Up to head dim 128 and   \
        without a mask all 32 exponent arguments are formed before the first exponential (SAGE_PHASE_FENCE):  \
@@ -481,11 +496,19 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       _Pragma("unroll") for (int i_ = 0; i_ < NPV; ++i_)                                                   \
         _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) o[i_][v_] *= corr_;                              \
     }                                                                                                      \
-    l = (corr_ * l + psum0_) + psum1_;                                                                     \
+    /* a speculative pass stands only if every lane's sum of its 16 probabilities of each block is below 2^7.5: \
+       then every p is, so no row's block max exceeds m by the rescale threshold 2^8 and the reference keeps m. \
+       Otherwise the pass adds nothing (l stays, the E4M3 bytes are zeroed so the MFMA adds +-0 to O, which \
+       never holds -0) and the tile runs as an exact pass. */                                              \
+    const bool sfail_ = spec_ && __ballot(!(psum0_ < SPEC_SUM && psum1_ < SPEC_SUM)) != 0;                 \
+    if (!sfail_) l = (corr_ * l + psum0_) + psum1_;                                                        \
     _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                     \
       const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                         \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
       pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);        \
+    }                                                                                                      \
+    if (sfail_) {                                                                                          \
+      _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) pb[w_] = 0;                                         \
     }                                                                                                      \
     __builtin_amdgcn_s_setprio(1);                                                                         \
     _Pragma("unroll") for (int j_ = 0; j_ < NPV; ++j_) {                                                   \
@@ -495,23 +518,26 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       o[j_] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va_, pb, o[j_], 0, 0, 0, 0, 0, 0);           \
     }                                                                                                      \
     __builtin_amdgcn_s_setprio(0);                                                                         \
-    redo_ = slow_;                                                                                         \
+    next_ = sfail_ ? PASS_EXACT : (slow_ ? PASS_REDO : PASS_NONE);                                         \
   } while (0)
 
-  // The tile's passes: one, or two when some lane of the wave moves its max at block 1 (the body sets redo_).  The
+  // The tile's passes: one, or more when a speculative pass does not stand or some lane of the wave moves its max
+  // at block 1 (the body sets next_: speculative -> exact -> redo, each at most once).  The
   // memory clobber keeps the LDS operand reads inside the loop, and the tile's mask word and bias values pass through
   // empty asm statements on every pass so that nothing derived from them (32 bit masks, 32 scaled biases) is hoisted
   // out of the loop and held across the whole body.
 #define SAGE_TILE_PASSES(T, MODE, MW, BW)                                                                   \
   do {                                                                                                     \
-    bool redo_ = false;                                                                                    \
-    _Pragma("nounroll") for (int pass_ = 0;; ++pass_) {                                                    \
+    int kind_ = (SPEC_OK && fastok) ? PASS_SPEC : PASS_EXACT;                                              \
+    int next_ = PASS_NONE;                                                                                 \
+    _Pragma("nounroll") for (;;) {                                                                         \
       asm volatile("" ::: "memory");                                                                       \
       uint32_t mwp_ = (MW);                                                                                \
       if ((MODE) == 2) asm volatile("" : "+v"(mwp_));                                                      \
       if ((MODE) == 3) asm volatile("" : "+v"((BW)[0]), "+v"((BW)[1]), "+v"((BW)[2]), "+v"((BW)[3]));      \
-      SAGE_TILE(T, MODE, mwp_, BW, pass_ > 0);                                                             \
-      if (!redo_) break;                                                                                   \
+      SAGE_TILE(T, MODE, mwp_, BW, kind_);                                                                 \
+      if (next_ == PASS_NONE) break;                                                                       \
+      kind_ = next_;                                                                                       \
     }                                                                                                      \
   } while (0)
 

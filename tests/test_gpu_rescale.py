@@ -7,6 +7,12 @@ those tiles in two passes (block 0 alone, then block 1 with its rescale first); 
 decisions once per 32-key block (kernel_build/make_sage_r2.py:180-190).  Each case checks, on the CPU, that the
 inputs really contain such block-1 rescales.
 
+Plateau inputs: from the second 64-key tile on, the even query rows see keys about 6.5 log2 units above the first
+tile's max, never the 8 that moves it.  Once a wave's rows all have a max, the kernel starts each tile with a
+speculative pass (no block maxima; it stands when every lane's sum of 16 probabilities is below 2^7.5); here those
+sums reach ~900, so the speculative passes do not stand, the exact passes find no row whose max moves, and the
+results must still be the reference's.  The case checks, on the CPU, that such tiles occur.
+
 Head dim 256: Q and K with one dominant channel per 128-channel rotation block, anti-aligned, quantize to
 S = Q8 K8^T down to -127^2 * 256 = -4,129,024, below the range a seeded fp32 read of the int32 accumulator covers
 (S >= -2,292,099); the kernel converts S exactly there.  Dense, additive-mask and varlen paths.
@@ -125,6 +131,79 @@ def test_block1_rescales_with_masks(dev):
         ref = orc.sdpa_reference(qn, kn, vn, attn_mask=m)
         assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
 
+
+
+def _plateau(B, H, Hkv, S, D, dt, seed, rise=6.5):
+    """Even query rows carry a shared direction u (|u|^2 = D) plus small noise; keys from 64 on carry c * u with
+    c * sqrt(D) * log2(e) = rise, so those rows' logits sit `rise` log2 units above the first tile's."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm() * math.sqrt(D)
+    q = torch.randn(B, H, S, D, generator=g) * 0.2
+    q[:, :, 0::2] += u
+    k = torch.randn(B, Hkv, S, D, generator=g) * 0.2
+    k[:, :, 64:] += rise / (math.sqrt(D) * math.log2(math.e)) * u
+    v = torch.randn(B, Hkv, S, D, generator=g)
+    return q.to(dt), k.to(dt), v.to(dt)
+
+
+def _speculative_false_alarms(q8, qs, k8, ks, seq_kv, causal):
+    """(wave of 32 query rows, 64-key tile) pairs in which every row has a max before the tile, some lane's sum of
+    its 16 probabilities of a 32-key block (keys 32 kb + 4 hf + 8 g + r, g, r < 4) reaches 181, and the reference's
+    decisions move no row's max: the speculative passes that must give way to an exact pass that changes nothing."""
+    B, H, Sq, D = q8.shape
+    hk = np.arange(H) // (H // k8.shape[1])
+    cl = (orc.logit_scale_base(D) * qs).astype(np.float32)
+    s = np.matmul(q8.astype(np.float32), np.swapaxes(k8.astype(np.float32)[:, hk], -1, -2))
+    cols = np.arange(s.shape[-1])
+    mask = cols[None, :] >= seq_kv
+    if causal:
+        mask = mask | (cols[None, :] > np.arange(Sq)[:, None] + seq_kv - Sq)
+    s = np.where(mask, -np.inf, s)
+    ksx = np.repeat(ks[:, hk], 32, axis=-1)[..., :s.shape[-1]]
+    lane = [np.array([32 * kb + 4 * hf + 8 * g + r for g in range(4) for r in range(4)]) for kb in (0, 1)
+            for hf in (0, 1)]
+    m = np.full((B, H, Sq), -np.inf, np.float32)
+    count = 0
+    for t in range(s.shape[-1] // 64):
+        blk = s[..., 64 * t: 64 * t + 64] * ksx[..., None, 64 * t: 64 * t + 64]
+        m_prev = m.copy()
+        moved = np.zeros_like(m, dtype=bool)
+        for kb in (0, 1):
+            mc = np.maximum(m, blk[..., 32 * kb: 32 * kb + 32].max(-1))
+            with np.errstate(invalid="ignore"):
+                need = (mc - m) * cl > 8
+            moved |= need
+            m = np.where(need, mc, m)
+        with np.errstate(invalid="ignore", over="ignore"):
+            p = np.exp2((blk - m_prev[..., None]) * cl[..., None])
+        big = np.zeros_like(moved)
+        for keys in lane:
+            big |= p[..., keys].sum(-1) >= 181.0
+        for w in range(0, Sq, 32):
+            rows = slice(w, min(w + 32, Sq))
+            finite = np.isfinite(m_prev[..., rows]).all(-1)
+            count += int((finite & big[..., rows].any(-1) & ~moved[..., rows].any(-1)).sum())
+    return count
+
+
+@pytest.mark.parametrize("D,dt,causal", [(128, torch.bfloat16, False), (64, torch.float16, True)])
+def test_speculative_passes_that_do_not_stand(dev, D, dt, causal):
+    B, H, S = 1, 2, 400
+    q, k, v = _plateau(B, H, H, S, D, dt, seed=7 + D)
+    qn, kn, vn = hnd_np(q), hnd_np(k), hnd_np(v)
+    q8, qs = orc.quant_q(qn)
+    k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(S))
+    assert _speculative_false_alarms(q8, qs, k8, ks, S, causal) >= 20
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), "HND", is_causal=causal)
+    got = hnd_np(out)
+    split = kv_split(dev, B, H, S, S, D, causal)
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, S, causal=causal, block_n=32, out_dtype="bf16" if dt == torch.bfloat16
+                        else "f16", kv_split=split)
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS and err <= 1e-2 * float(np.abs(emu).max()), err
+    ref = orc.sdpa_reference(qn, kn, vn, causal=causal)
+    assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
 
 def _anti_aligned_d256(B, H, Hkv, Sq, Skv, dt, seed):
     """Q rows with one dominant channel in each 128-channel block; K rows with the same channels negated and scaled
