@@ -8,9 +8,11 @@
 // wave needs masked run a mask-free body).  Per wave and tile,
 // S^T = K Q^T with v_mfma_f32_32x32x16_{bf16,f16}: A = 32 keys x 16 dims of K from LDS, B = Q from registers.  The
 // accumulator gives lane l the query l % 32 and 16 keys of each 32-key block, so the row statistics need one exchange
-// with lane l ^ 32.  Statistics are exact online max / sum in the log2 domain (no lazy threshold: there is no output
-// accumulator to rescale): m = max_j s_ij, l = sum_j 2^((s_ij - m) * c) with c = sm_scale * log2(e), and
-// lse = ln 2 * (m * c + log2 l).  Causal masks are bottom-right aligned (Sq <= Skv).
+// with lane l ^ 32.  Statistics are an online max / sum in the log2 domain: l = sum_j 2^((s_ij - m) * c) with
+// c = sm_scale * log2(e) and lse = ln 2 * (m * c + log2 l), for any m that keeps the terms finite.  m is the running
+// max, raised only when needed: once every row of a wave has one, a tile first adds its terms with the current m and
+// keeps them when every lane's sum is below 2^16 (almost always; an overflow gives inf and fails the test), else it
+// takes the tile's max as the exact online update does.  Causal masks are bottom-right aligned (Sq <= Skv).
 #include <type_traits>
 
 #include "sage_common.h"
@@ -126,6 +128,8 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
   for (int i = 0; i < NK; ++i) ko[i] = ln * ROWB + lse_swz<KCH>(ln, 2 * i + hf) * 16;
 
   float m = -INFINITY, l = 0.0f;
+  float negm = 0.0f;    // -(m * c) once m is finite
+  bool fastok = false;  // every row of the wave has a finite m: tiles start with the current m
   // One tile: S^T from the LDS buffer, the MASKED body clears keys past Skv and (causal) past the row's diagonal.
   // The two bodies sit in two loops (tiles before t_mask need no mask for any row of the wave): with the mask test
   // in one loop the compiler turns the masking into compares and selects on every tile.
@@ -155,22 +159,37 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
         for (int v = 0; v < 16; ++v)
           if (32 * kb + 8 * (v >> 2) + (v & 3) > lim) sv[kb][v] = -INFINITY;
     }
-    float mx = sv[0][0];
+    bool exact = !fastok;
+    if (fastok) {
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sv[0][v]);
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sv[1][v]);
-    mx = max_xor32_f32(mx);
-    const float m_new = fmaxf(m, mx);
-    const float corr = __builtin_amdgcn_exp2f((m - m_new) * c);  // m = -inf on the first tile: corr = 0
-    const float neg = 0.0f - m_new * c;
-    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int v = 0; v < 16; ++v) ps[v & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, negm));
+      const float tsum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      exact = __ballot(!(tsum < 65536.0f)) != 0;
+      if (!exact) l = l + tsum;
+    }
+    if (exact) {
+      float mx = sv[0][0];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sv[0][v]);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) ps[v & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, neg));
-    l = l * corr + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
-    m = m_new;
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sv[1][v]);
+      mx = max_xor32_f32(mx);
+      const float m_new = fmaxf(m, mx);
+      const float corr = __builtin_amdgcn_exp2f((m - m_new) * c);  // m = -inf on the first tile: corr = 0
+      const float neg = 0.0f - m_new * c;
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) ps[v & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, neg));
+      l = l * corr + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      m = m_new;
+      negm = m == -INFINITY ? 0.0f : neg;  // a row with no visible key yet keeps m = -inf
+      fastok = __ballot(m == -INFINITY) == 0;
+    }
     // the wait for the next tile's direct loads comes after this tile's arithmetic (l is its last result; without
     // the operand the scheduler may hoist the wait into the middle of the tile)
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(l) : : "memory");
