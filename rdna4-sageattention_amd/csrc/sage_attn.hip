@@ -500,15 +500,19 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
        then every p is, so no row's block max exceeds m by the rescale threshold 2^8 and the reference keeps m. \
        Otherwise the pass adds nothing (l stays, the E4M3 bytes are zeroed so the MFMA adds +-0 to O, which \
        never holds -0) and the tile runs as an exact pass. */                                              \
-    const bool sfail_ = spec_ && __ballot(!(psum0_ < SPEC_SUM && psum1_ < SPEC_SUM)) != 0;                 \
-    if (!sfail_) l = (corr_ * l + psum0_) + psum1_;                                                        \
-    _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                     \
-      const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                         \
-      pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);           \
-      pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);        \
-    }                                                                                                      \
+    /* one ballot per compare: each is the compare's lane mask, where a ballot of their OR costs a select */ \
+    const uint64_t big_ = __builtin_amdgcn_ballot_w64(!(psum0_ < SPEC_SUM)) |                              \
+                          __builtin_amdgcn_ballot_w64(!(psum1_ < SPEC_SUM));                               \
+    const bool sfail_ = spec_ && big_ != 0;                                                                \
     if (sfail_) {                                                                                          \
       _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) pb[w_] = 0;                                         \
+    } else {                                                                                               \
+      l = (corr_ * l + psum0_) + psum1_;                                                                   \
+      _Pragma("unroll") for (int w_ = 0; w_ < 8; ++w_) {                                                   \
+        const int kb_ = w_ >> 2, v0_ = 4 * (w_ & 3);                                                       \
+        pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_], sf_[kb_][v0_ + 1], pb[w_], false);         \
+        pb[w_] = __builtin_amdgcn_cvt_pk_fp8_f32(sf_[kb_][v0_ + 2], sf_[kb_][v0_ + 3], pb[w_], true);      \
+      }                                                                                                    \
     }                                                                                                      \
     __builtin_amdgcn_s_setprio(1);                                                                         \
     _Pragma("unroll") for (int j_ = 0; j_ < NPV; ++j_) {                                                   \
