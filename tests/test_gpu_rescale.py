@@ -280,3 +280,37 @@ def test_head_dim_256_extreme_scores_varlen(dev):
         hnd = lambda t: np.ascontiguousarray(t.float().numpy().transpose(1, 0, 2))[None]   # noqa: E731
         ref = orc.sdpa_reference(hnd(q[q0:q1]), hnd(k[k0:k1]), hnd(v[k0:k1]))[0].transpose(1, 0, 2)
         assert cosine(got[q0:q1], ref) >= COS
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_staircase_and_plateau(dev, causal):
+    """The packed variable-length kernel runs the same tile passes: a staircase sequence (block-1 rescales after
+    the first tile) and a plateau sequence (speculative passes that do not stand) in one batch."""
+    H, Hkv, D = 4, 2, 128
+    lq, lk = [300, 260], [300, 400]
+    gens = [lambda a, b: _staircase(1, H, Hkv, max(a, b), D, torch.bfloat16, seed=70 + causal),
+            lambda a, b: _plateau(1, H, Hkv, max(a, b), D, torch.bfloat16, seed=80 + causal)]
+    qs_, ks_, vs_ = [], [], []
+    for g, a, b in zip(gens, lq, lk):
+        q, k, v = g(a, b)
+        qs_.append(q[0, :, :a].transpose(0, 1))
+        ks_.append(k[0, :, :b].transpose(0, 1))
+        vs_.append(v[0, :, :b].transpose(0, 1))
+    q, k, v = (torch.cat(t).contiguous() for t in (qs_, ks_, vs_))          # [total, heads, D]
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
+    # the inputs do contain both kinds of tile (counted per sequence on the CPU)
+    hnd = lambda t: np.ascontiguousarray(t.float().numpy().transpose(1, 0, 2))[None]   # noqa: E731
+    q8a, qsa = orc.quant_q(hnd(q[:lq[0]]))
+    k8a, ksa, _, _ = orc.quant_kv(hnd(k[:lk[0]]), hnd(v[:lk[0]]), seq_pad=_capi.kv_pad(lk[0]))
+    assert _block1_rescales(q8a, qsa, k8a, ksa, lk[0], causal) >= 50
+    q8b, qsb = orc.quant_q(hnd(q[lq[0]:]))
+    k8b, ksb, _, _ = orc.quant_kv(hnd(k[lk[0]:]), hnd(v[lk[0]:]), seq_pad=_capi.kv_pad(lk[1]))
+    assert _speculative_false_alarms(q8b, qsb, k8b, ksb, lk[1], causal) >= 10
+    out = cdna4_sage.attention_varlen(q.to(dev), k.to(dev), v.to(dev), torch.tensor(cu_q, device=dev),
+                                      torch.tensor(cu_k, device=dev), max(lq), max(lk), is_causal=causal)
+    emu = orc.sage_forward_varlen(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q, cu_k,
+                                  causal=causal, block_n=32, out_dtype="bf16")
+    got = out.float().cpu().numpy()
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS and err <= 1e-2 * float(np.abs(emu).max()), err
