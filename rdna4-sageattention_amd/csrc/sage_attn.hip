@@ -148,10 +148,11 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   constexpr float SEED_F = __builtin_bit_cast(float, SEED_BITS);
   constexpr float SSCALE = SEEDED ? 67108864.0f : 1.0f;  // 2^26
   // Passes of a tile body: speculative (the offsets of the current m, no block maxima), exact (the block maxima and
-  // the reference's rescale decisions), and the redo of block 1 after a block-1 rescale.  The mask variant and head
-  // dim 256 (which would spill with the speculative code) have no speculative pass.
+  // the reference's rescale decisions), and the redo of block 1 after a block-1 rescale.  Head dim 256 (which would
+  // spill with the speculative code) and the additive-mask body (MODE 3, whose row maxima are taken over the biased
+  // logits it forms in the same loop) have no speculative pass.
   constexpr int PASS_NONE = 0, PASS_SPEC = 1, PASS_EXACT = 2, PASS_REDO = 3;
-  constexpr bool SPEC_OK = !MASK && HD <= 128;
+  constexpr bool SPEC_OK = HD <= 128;
   constexpr float SPEC_SUM = 181.0f;  // below 2^7.5: a margin of 2^0.5 under the threshold for fp32 rounding
   // K / V tile buffers: three where they fit (the unmasked loops prefetch two tiles ahead, which hides the direct
   // loads' latency behind two tiles of arithmetic), two for head dim 256 (3 x 32 KiB per workgroup would leave room
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     float corr_ = 1.0f;     /* the rescale before this pass's MFMA */                                      \
     bool slow_ = false;     /* some lane moves its max at block 1 in a first pass: block 1 waits for pass 1 */ \
     bool resc_ = false;     /* some lane rescales O before this pass's MFMA */                             \
-    const bool spec_ = SPEC_OK && (KIND) == PASS_SPEC;                                                     \
+    const bool spec_ = SPEC_OK && (MODE) != 3 && (KIND) == PASS_SPEC;                                      \
     if (!spec_) {                                                                                          \
       /* the two 32-key blocks' row maxima, one per lane half (block hf's, for row ln): MODE 3 in log2 units of the \
          biased logits t (kept in sf_), else in m's units, fp32(max S * ks) (scaled by 2^-26 when seeded: mx - c is \
