@@ -71,6 +71,10 @@ LOG2E = 1.4426950408889634  # the reference's _LOG2E (python float)
 # sum read as fp32 is c + S * 2^-26 exactly for -2,292,099 <= S <= 6,096,509 (see seeded()), so it needs no conversion
 SEED = float(np.array([0x3E22F983], dtype=np.uint32).view(np.float32)[0])
 SEED_ULP = 2.0 ** -26
+# Large scales: a 32-row group (a wave) whose largest K scale over the keys exceeds fp32(CT_WIDE / its largest
+# cl * 2^26) reads its scores exactly (F - c) with the offset -(cl * m), the reference's form; the seeded form's
+# rounding of c * ct grows with ct
+CT_WIDE = 2.0 ** 18
 # the gfx950 kernel's key tile: split key ranges and the classes of additive masks are per 64-key tile, whatever the
 # block_n of the online softmax
 KERNEL_TILE = 64
@@ -321,11 +325,13 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
         qpos = (np.asarray(q_rows, dtype=np.int64), int(seq_q))
     else:
         qpos = (np.arange(q8.shape[2]), q8.shape[2])
-    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask, qpos)
+    wide = wide_rows(cl, ks, seq_kv, qpos[0], hk) if seeded(D) else None
+    o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask, qpos,
+                              wide)
     if kv_split is not None:
         chunks, rows = kv_split
         parts = [_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold,
-                                 *krange(c, chunks), attn_mask, qpos)
+                                 *krange(c, chunks), attn_mask, qpos, wide)
                  for c in range(chunks)]
         mm = parts[0][1]
         for _, mc, _ in parts[1:]:
@@ -354,8 +360,23 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     return out
 
 
+def wide_rows(cl, ks, seq_kv, pos, hk):
+    """Bool [B, H, Sq]: rows whose 32-row group (query positions pos // 32; with a sample of rows, the sampled rows
+    of the group) reads its scores in the reference's form: the largest K scale of its kv head over the blocks of
+    keys [0, seq_kv) exceeds fp32(CT_WIDE / the group's largest cl * 2^26).  cl [B, H, Sq], ks [B, Hkv, Sp/32]."""
+    cls = (cl * F32(2.0 ** 26)).astype(F32)
+    kmx = ks[:, :, :(seq_kv + KV_BLOCK - 1) // KV_BLOCK].astype(F32).max(axis=-1)[:, hk]      # [B, H]
+    grp = np.asarray(pos) // 32
+    out = np.zeros(cls.shape, dtype=bool)
+    for g in np.unique(grp):
+        sel = grp == g
+        thr = (F32(CT_WIDE) / cls[..., sel].max(axis=-1)).astype(F32)                      # [B, H]
+        out[..., sel] = (kmx > thr)[..., None]
+    return out
+
+
 def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi, attn_mask=None,
-                    qpos=None):
+                    qpos=None, wide=None):
     """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row.  attn_mask:
     None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).  qpos:
     (the rows' positions in the query sequence, its length), default all Sq rows.
@@ -430,17 +451,22 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
             ct = (ct * F32(2.0 ** 26)).astype(F32)
             nk = (neg[..., None] - (F32(SEED) * ct).astype(F32)).astype(F32)
             fs = (sb * F32(SEED_ULP) + F32(SEED)).astype(F32)
+            # rows of a wide group: F - c = S * 2^-26 (exact) and the offset without the seed term
+            wb = np.broadcast_to(wide[..., None], ct.shape)                     # [B, H, Sq, nsub]
+            nk = np.where(wb, neg[..., None], nk).astype(F32)
+            fs = np.where(wb[..., None], (sb * F32(SEED_ULP)).astype(F32), fs).astype(F32)
+            seed_t = np.where(wb, F32(0.0), F32(SEED)).astype(F32)
         else:
             # head dim 256: F = fp32(S), arg = fma(S, ct, neg), the reference's exponent (make_sage_r2.py:193-200).
             # S * ct is exact in float64; the sum is rounded twice (float64, then float32), which differs from the
             # fma's single rounding only when the float64 result lands on a float32 rounding boundary.
             nk = np.broadcast_to(neg[..., None], ct.shape).astype(F32)
             fs = sb.astype(F32)
+            seed_t = F32(0.0)
         arg = (fs.astype(np.float64) * ct[..., None].astype(np.float64) + nk[..., None].astype(np.float64)).astype(F32)
         p = np.exp2(arg).astype(F32).reshape(B, H, Sq, block_n)
         if bias_rows is not None and bias_rows.any():
-            p, corr, need, m_new = _bias_tile(fs, ct, bt, m, cl, threshold, bias_rows, p, corr, need, m_new,
-                                              SEED if seeded(D) else 0.0)
+            p, corr, need, m_new = _bias_tile(fs, ct, bt, m, cl, threshold, bias_rows, p, corr, need, m_new, seed_t)
         tile_sum = p.sum(axis=-1, dtype=F32)
         l = ((corr * l).astype(F32) + tile_sum).astype(F32)
         o = np.where(need[..., None], (o * corr[..., None]).astype(F32), o)
@@ -453,7 +479,8 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
 def _bias_tile(fs, ct, bt, m, cl, threshold, rows, p, corr, need, m_new, seed=SEED):
     """The bias path of one tile for the rows in `rows` (other rows keep p, corr, need, m_new as given).  fs: the
     scores as the kernel reads them [B, H, Sq, nsub, 32]; ct [B, H, Sq, nsub] (scaled by 2^26 like the kernel's
-    when seeded); bt: the additive mask of the tile [B, H, Sq, block_n]; seed: c, or 0 for unseeded scores."""
+    when seeded); bt: the additive mask of the tile [B, H, Sq, block_n]; seed: c, or 0 for unseeded scores and wide
+    blocks (a scalar or [B, H, Sq, nsub])."""
     B, H, Sq = m.shape
     nsub = ct.shape[-1]
     f64 = np.float64

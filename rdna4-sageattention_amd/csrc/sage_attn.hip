@@ -154,6 +154,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   constexpr int PASS_NONE = 0, PASS_SPEC = 1, PASS_EXACT = 2, PASS_REDO = 3;
   constexpr bool SPEC_OK = HD <= 128;
   constexpr float SPEC_SUM = 181.0f;  // below 2^7.5: a margin of 2^0.5 under the threshold for fp32 rounding
+  constexpr float CT_WIDE = 262144.0f;  // 2^18: the largest ct (scaled by 2^26) read through the seeded form
   // K / V tile buffers: three where they fit (the unmasked loops prefetch two tiles ahead, which hides the direct
   // loads' latency behind two tiles of arithmetic), two for head dim 256 (3 x 32 KiB per workgroup would leave room
   // for one workgroup per CU) and for the mask variant (whose loops prefetch one tile ahead)
@@ -222,9 +223,38 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
 #pragma unroll
     for (int i = 0; i < NQK; ++i) qa[i] = *reinterpret_cast<const v4i*>(qp + 32 * i);
   }
+  const float qsv = qs[qrow0 + qr];
+  // The K scales of the keys [0, Skv), whose maximum decides `wide` below: the first 256 blocks loaded four per lane
+  // beside the Q operand and its scale (one wait for all), the rest (long key ranges only) eight per lane at a time
+  const float* ksq = ks + ((int64_t)khead * Skp + kofs) / SAGE_KV_BLOCK;
+  const int nkb = (Skv + SAGE_KV_BLOCK - 1) / SAGE_KV_BLOCK;
+  float kq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (SEEDED) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) kq[u] = ksq[min(64 * u + lane, nkb - 1)];
+  }
   // cl of the math scaled by SSCALE, m in units of S * ks / SSCALE (the seeded accumulators below hold S * 2^-26)
-  const float cl = (c0 * qs[qrow0 + qr]) * SSCALE;
+  const float cl = (c0 * qsv) * SSCALE;
   const float rcl = 1.0f / cl;  // the bias tiles keep m in S * ks * 2^-26 units
+  // Large scales.  The seeded exponent argument fma(F, ct, -(cl * m) - fp32(c * ct)) carries the rounding of c * ct,
+  // up to ~1.5 ct * 2^-26 log2 units, which grows with the input scale (~2^-9 at ct = 2^18; the benchmark inputs
+  // stay below 2.5e4).  A wave whose largest K scale of the keys [0, Skv) exceeds fp32(CT_WIDE / its largest cl)
+  // reads its scores exactly instead, F - c = S * 2^-26 (Sterbenz), with the offset -(cl * m): the reference's
+  // fma(S, cl * ks, -cl * m).  Decided once per work unit; both maxima are of positive floats, so their bit
+  // patterns order like unsigned ints.
+  bool wide = false;
+  if (SEEDED) {
+    float km = fmaxf(fmaxf(kq[0], kq[1]), fmaxf(kq[2], kq[3]));
+    for (int j0 = 256; j0 < nkb; j0 += 512) {
+      float kx[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kx[u] = ksq[min(j0 + 64 * u + lane, nkb - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) km = fmaxf(km, kx[u]);
+    }
+    const float cmx = wave_max_pos(cl), kmx = wave_max_pos(km);
+    wide = kmx > CT_WIDE / cmx;
+  }
 
   // ---- KV range ----
   int kv_end = Skv;
@@ -260,7 +290,6 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   const int8_t* kbase = k8 + ((int64_t)khead * Skp + kofs) * D;
   const uint8_t* vbase = v8t + (int64_t)khead * D * Skp + kofs;
   const float* ksb = ks + ((int64_t)khead * Skp + kofs) / SAGE_KV_BLOCK;
-
   // Source of each lane's direct loads.  Load j of wave w fills LDS chunk L = (w * LOADS + j) * 64 + lane of the
   // region, which must receive the tile chunk that the swizzled layout stores there.
   uint32_t koff[KLOADS];
@@ -336,7 +365,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   // sits in a branch: around one the compiler
   // loses the accumulators' coalescing and spills the whole loop; the O rescale sits in its own branch after the
   // exponentials for the same reason.
-#define SAGE_TILE(T, MODE, MW, BW, KIND)                                                                       \
+#define SAGE_TILE(T, MODE, MW, BW, KIND, WIDE)                                                             \
   do {                                                                                                     \
     const int t_ = (T);                                                                                    \
     const uint8_t* kt_ = smem[t_ % NBUF];                                                                  \
@@ -393,7 +422,12 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       if ((MODE) == 3) {                                                                                   \
         /* t = fma(F, ct, fma(b, log2e, -fp32(c * ct))) (b = -inf for a masked key gives -inf); the lazy   \
            rescale compares a block's max of t with m * cl and keeps m in S * ks units (m_new = m_cand / cl) */ \
-        const float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;    \
+        float ns0_ = SEEDED ? -(SEED_F * ct0_) : -0.0f, ns1_ = SEEDED ? -(SEED_F * ct1_) : -0.0f;          \
+        if (WIDE) {  /* exact scores, no seed term */                                                      \
+          ns0_ = ns1_ = -0.0f;                                                                             \
+          _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                              \
+            _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] -= SEED_F;                      \
+        }                                                                                                  \
         float tm0_ = -INFINITY, tm1_ = -INFINITY;                                                          \
         _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                \
           _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                              \
@@ -479,6 +513,14 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
        without a mask all 32 exponent arguments are formed before the first exponential (SAGE_PHASE_FENCE):  \
        interleaved, each v_exp_f32 waits on the FMA just before it, which three waves per SIMD do not hide.   \
        The mask variant (three tile bodies) and head dim 256 hold more registers and would spill with it. */ \
+    /* a wide wave reads F - c after the block maxima (which order the seeded patterns as ints) and drops the \
+       seed term: the offsets are then -(cl * m) after this pass's update, -inf for a slow pass's block 1 */ \
+    if ((MODE) != 3 && (WIDE)) {                                                                           \
+      nk0_ = negm;                                                                                         \
+      nk1_ = slow_ ? -INFINITY : negm;                                                                     \
+      _Pragma("unroll") for (int kb_ = 0; kb_ < 2; ++kb_)                                                  \
+        _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) sf_[kb_][v_] -= SEED_F;                          \
+    }                                                                                                      \
     float psum0_, psum1_;                                                                                  \
     _Pragma("unroll") for (int v_ = 0; v_ < 16; ++v_) {                                                    \
       sf_[0][v_] = (MODE) == 3 ? sf_[0][v_] + nk0_ : __builtin_fmaf(sf_[0][v_], ct0_, nk0_);               \
@@ -531,7 +573,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   // memory clobber keeps the LDS operand reads inside the loop, and the tile's mask word and bias values pass through
   // empty asm statements on every pass so that nothing derived from them (32 bit masks, 32 scaled biases) is hoisted
   // out of the loop and held across the whole body.
-#define SAGE_TILE_PASSES(T, MODE, MW, BW)                                                                   \
+#define SAGE_TILE_PASSES(T, MODE, MW, BW, WIDE)                                                            \
   do {                                                                                                     \
     int kind_ = (SPEC_OK && fastok) ? PASS_SPEC : PASS_EXACT;                                              \
     int next_ = PASS_NONE;                                                                                 \
@@ -540,7 +582,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
       uint32_t mwp_ = (MW);                                                                                \
       if ((MODE) == 2) asm volatile("" : "+v"(mwp_));                                                      \
       if ((MODE) == 3) asm volatile("" : "+v"((BW)[0]), "+v"((BW)[1]), "+v"((BW)[2]), "+v"((BW)[3]));      \
-      SAGE_TILE(T, MODE, mwp_, BW, kind_);                                                                 \
+      SAGE_TILE(T, MODE, mwp_, BW, kind_, WIDE);                                                           \
       if (next_ == PASS_NONE) break;                                                                       \
       kind_ = next_;                                                                                       \
     }                                                                                                      \
@@ -582,7 +624,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           c_nxt = mcls[t + 1];
           SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
         }
-        if (c_cur == 1) SAGE_TILE_PASSES(t, 0, 0u, bw_none);
+        if (c_cur == 1) SAGE_TILE_PASSES(t, 0, 0u, bw_none, wide);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
@@ -600,7 +642,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
             c_nxt = mcls[t + 1];
             SAGE_ISSUE_TILE(t + 1, (t + 1) & 1);
           }
-          SAGE_TILE_PASSES(t, 2, mw_cur, bw_none);
+          SAGE_TILE_PASSES(t, 2, mw_cur, bw_none, wide);
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           asm volatile("" ::"v"(mw_nxt));
           __syncthreads();
@@ -619,7 +661,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
         const int tn_ = min(t + 1, t_hi - 1);
         c_nxt = mcls[tn_];
         SAGE_ISSUE_TILE(tn_, (t + 1) & 1);
-        SAGE_TILE_PASSES(t, 3, 0u, bias_w);
+        SAGE_TILE_PASSES(t, 3, 0u, bias_w, wide);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       }
@@ -628,18 +670,26 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     // tile t + NBUF - 1 goes into the buffer tile t - 1 used, which every wave left at the last barrier; the end of
     // tile t waits for tile t + 1 (all but the LPT loads of tile t + 2 when those were issued: loads complete in order)
     constexpr int PF = NBUF - 1;
-    for (; t < t_mask; ++t) {
-      const bool ahead = t + PF < t_hi;
-      if (ahead) SAGE_ISSUE_TILE(t + PF, (t + PF) % NBUF);
-      SAGE_TILE_PASSES(t, 0, 0u, bw_none);
-      if (PF == 2 && ahead) wait_vmcnt<LPT>();
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      tile_barrier();
+    // the mask-free loop in two copies, so that its tiles carry no test of `wide`
+#define SAGE_MASK_FREE_LOOP(WIDE)                                                                          \
+    for (; t < t_mask; ++t) {                                                                              \
+      const bool ahead = t + PF < t_hi;                                                                    \
+      if (ahead) SAGE_ISSUE_TILE(t + PF, (t + PF) % NBUF);                                                 \
+      SAGE_TILE_PASSES(t, 0, 0u, bw_none, WIDE);                                                           \
+      if (PF == 2 && ahead) wait_vmcnt<LPT>();                                                             \
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                                \
+      tile_barrier();                                                                                      \
     }
+    if (wide) {
+      SAGE_MASK_FREE_LOOP(true);
+    } else {
+      SAGE_MASK_FREE_LOOP(false);
+    }
+#undef SAGE_MASK_FREE_LOOP
     for (; t < t_hi; ++t) {
       const bool ahead = t + PF < t_hi;
       if (ahead) SAGE_ISSUE_TILE(t + PF, (t + PF) % NBUF);
-      SAGE_TILE_PASSES(t, 1, 0u, bw_none);
+      SAGE_TILE_PASSES(t, 1, 0u, bw_none, wide);
       if (PF == 2 && ahead) wait_vmcnt<LPT>();
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       tile_barrier();

@@ -52,6 +52,8 @@ template <int DT> __device__ __forceinline__ uint32_t f32_to_out_bits(float f) {
 // DPP quad_perm selectors: lane i of each quad reads lane sel[i].
 constexpr int DPP_QUAD_XOR1 = 0xB1;  // [1, 0, 3, 2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;  // [2, 3, 0, 1]
+constexpr int DPP_ROW_ROR4 = 0x124;  // each 16-lane row rotated by 4 lanes
+constexpr int DPP_ROW_ROR8 = 0x128;  // each 16-lane row rotated by 8 lanes
 
 // (quad_perm reads a valid lane for every lane, so the DPP "old" value is never used: mov_dpp needs no copy of it)
 template <int CTRL> __device__ __forceinline__ float dpp_f32(float x) {
@@ -62,6 +64,20 @@ template <int CTRL> __device__ __forceinline__ double dpp_f64(double x) {
   const int plo = __builtin_amdgcn_mov_dpp(lo, CTRL, 0xF, 0xF, false);
   const int phi = __builtin_amdgcn_mov_dpp(hi, CTRL, 0xF, 0xF, false);
   return __hiloint2double(phi, plo);
+}
+
+// Maximum over the wave of a non-negative float, as a wave-uniform value: quad DPP exchanges, two rotations inside
+// each 16-lane row, then the four rows' values read into scalar registers (non-negative floats order like their
+// bit patterns as unsigned ints)
+__device__ __forceinline__ float wave_max_pos(float x) {
+  x = fmaxf(x, dpp_f32<DPP_QUAD_XOR1>(x));
+  x = fmaxf(x, dpp_f32<DPP_QUAD_XOR2>(x));
+  x = fmaxf(x, dpp_f32<DPP_ROW_ROR4>(x));
+  x = fmaxf(x, dpp_f32<DPP_ROW_ROR8>(x));
+  const uint32_t b = __float_as_uint(x);
+  const uint32_t r0 = __builtin_amdgcn_readlane(b, 0), r1 = __builtin_amdgcn_readlane(b, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(b, 32), r3 = __builtin_amdgcn_readlane(b, 48);
+  return __uint_as_float(max(max(r0, r1), max(r2, r3)));
 }
 
 // A scheduling fence for the 32 values of a wave's tile (float[2][16]): every value passes through this empty

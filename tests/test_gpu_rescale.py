@@ -314,3 +314,25 @@ def test_varlen_staircase_and_plateau(dev, causal):
     got = out.float().cpu().numpy()
     err = float(np.abs(got - emu).max())
     assert err <= MAX_ABS and err <= 1e-2 * float(np.abs(emu).max()), err
+
+
+@pytest.mark.parametrize("scale,D,causal", [(30.0, 128, False), (300.0, 128, True), (1000.0, 64, False)])
+def test_large_logits(dev, scale, D, causal):
+    """Inputs scaled so that the logits reach ~10^3-10^6 log2 units: the speculative pass's exponent arguments and
+    the reference's rescale test then differ by more fp32 rounding, the softmax is close to one-hot, and the output
+    must still follow the emulation within the usual bounds."""
+    B, H, S = 1, 2, 333
+    g = torch.Generator().manual_seed(int(scale) + D)
+    q = (torch.randn(B, H, S, D, generator=g) * scale).to(torch.bfloat16)
+    k = (torch.randn(B, H, S, D, generator=g) * scale).to(torch.bfloat16)
+    v = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), "HND", is_causal=causal)
+    got = hnd_np(out)
+    qn, kn, vn = hnd_np(q), hnd_np(k), hnd_np(v)
+    q8, qs = orc.quant_q(qn)
+    k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(S))
+    assert np.isfinite(got).all()
+    split = kv_split(dev, B, H, S, S, D, causal)
+    emu = orc.attention(q8, qs, k8, ks, v8, vs, S, causal=causal, block_n=32, kv_split=split)
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS and err <= 1e-2 * float(np.abs(emu).max()), err

@@ -254,6 +254,39 @@ def test_emulation_single_key_returns_dequantized_v():
     assert bound.max() < 1e-3
 
 
+
+def test_emulation_large_scales_read_scores_exactly(monkeypatch):
+    """Inputs scaled by 100: the seeded read's offset rounding (up to ~1.5 ct log2 units, ct the logit per unit of S)
+    would move a single key's p far from 1, so the rule reads such groups exactly (F - c) with the reference's
+    offset, arg = fp32(S * fp32(cl * ks) - fp32(cl * fp32(S * ks))), |arg| <= 3.1 * 2^-24 * |logit|.  At scale 1
+    the rule does not fire.  Planted mistake: without the rule (CT_WIDE = inf) the same bound fails."""
+    def run(scale):
+        q = _bf16((1, 2, 5, 64), 60) * scale
+        k = _bf16((1, 2, 1, 64), 61) * scale
+        v = _bf16((1, 2, 1, 64), 62)
+        q, k = orc.round_to_bf16(q), orc.round_to_bf16(k)
+        q8, qs = orc.quant_q(q)
+        k8, ks, v8, vs = orc.quant_kv(k, v)
+        cl = (orc.logit_scale_base(64) * qs).astype(np.float32)
+        wide = orc.wide_rows(cl, ks, 1, np.arange(5), np.arange(2))
+        out = orc.attention(q8, qs, k8, ks, v8, vs, 1, out_dtype="f32")
+        deq = orc.e4m3_to_f32(v8[:, :, :1]) * vs[:, :, None, :] / 448.0
+        s = np.matmul(q8.astype(np.float64), np.swapaxes(k8[:, :, :1].astype(np.float64), -1, -2))[..., 0]
+        logit = np.abs(s * cl.astype(np.float64) * ks[:, :, :1].astype(np.float64))            # [B, H, Sq]
+        bound = np.exp2(3.1 * 2.0 ** -24 * logit) - 1.0 + 1e-6
+        rel = np.abs(out / np.broadcast_to(deq, out.shape) - 1.0).max(axis=-1)
+        return wide, rel, bound
+    wide, rel, bound = run(1.0)
+    assert not wide.any()
+    wide, rel, bound = run(100.0)
+    assert wide.all() and np.isfinite(rel).all()
+    assert (rel <= bound).all(), (rel.max(), bound.min())
+    assert bound.max() < 0.02
+    monkeypatch.setattr(orc, "CT_WIDE", float("inf"))
+    wide, rel, bound = run(100.0)
+    assert not wide.any()
+    assert not (rel <= bound).all()
+
 def test_emulation_causal_first_row_and_bottom_right():
     q, k, v = _bf16((1, 1, 40, 64), 15), _bf16((1, 1, 40, 64), 16), _bf16((1, 1, 40, 64), 17)
     out = orc.sage_forward(q, k, v, causal=True, block_n=32, out_dtype="f32")
