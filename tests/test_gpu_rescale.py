@@ -336,3 +336,47 @@ def test_large_logits(dev, scale, D, causal):
     emu = orc.attention(q8, qs, k8, ks, v8, vs, S, causal=causal, block_n=32, kv_split=split)
     err = float(np.abs(got - emu).max())
     assert err <= MAX_ABS and err <= 1e-2 * float(np.abs(emu).max()), err
+
+
+@pytest.mark.parametrize("kind", ["bool", "bias", "varlen"])
+def test_large_logits_mask_and_varlen(dev, kind):
+    """The large-scale read (scores taken exactly, the reference's offset) in the mask variant's bit-masked and
+    additive-bias bodies and in the packed variable-length kernel."""
+    H, D, scale = 2, 128, 300.0
+    g = torch.Generator().manual_seed(91)
+    if kind == "varlen":
+        lq, lk = [150, 260], [200, 260]
+        q = (torch.randn(sum(lq), H, D, generator=g) * scale).to(torch.bfloat16)
+        k = (torch.randn(sum(lk), H, D, generator=g) * scale).to(torch.bfloat16)
+        v = torch.randn(sum(lk), H, D, generator=g).to(torch.bfloat16)
+        cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+        cu_k = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
+        out = cdna4_sage.attention_varlen(q.to(dev), k.to(dev), v.to(dev), torch.tensor(cu_q, device=dev),
+                                          torch.tensor(cu_k, device=dev), max(lq), max(lk))
+        got = out.float().cpu().numpy()
+        emu = orc.sage_forward_varlen(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q, cu_k,
+                                      block_n=32, out_dtype="bf16")
+    else:
+        B, S = 1, 300
+        q = (torch.randn(B, H, S, D, generator=g) * scale).to(torch.bfloat16)
+        k = (torch.randn(B, H, S, D, generator=g) * scale).to(torch.bfloat16)
+        v = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+        if kind == "bool":
+            mask = torch.rand(1, 1, S, S, generator=g) < 0.6
+            mask[..., 0] = True
+            m = mask.numpy()
+        else:
+            mask = ((torch.rand(1, 1, S, S, generator=g) - 0.5) * 8).to(torch.bfloat16)
+            m = mask.float().numpy()
+        out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), "HND", attn_mask=mask.to(dev))
+        got = hnd_np(out)
+        qn, kn, vn = hnd_np(q), hnd_np(k), hnd_np(v)
+        q8, qs = orc.quant_q(qn)
+        k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(S))
+        cl = (orc.logit_scale_base(D) * qs).astype(np.float32)
+        assert orc.wide_rows(cl, ks, S, np.arange(S), np.arange(H)).all()
+        split = kv_split(dev, B, H, S, S, D, False)
+        emu = orc.attention(q8, qs, k8, ks, v8, vs, S, block_n=32, kv_split=split, attn_mask=m)
+    assert np.isfinite(got).all()
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS and err <= 1e-2 * float(np.abs(emu).max()), err
