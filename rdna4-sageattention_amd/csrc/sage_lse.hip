@@ -161,11 +161,14 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
     }
     bool exact = !fastok;
     if (fastok) {
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float ps[4];  // four chains, each starting from its first term (0 + p is p: exp2 never gives -0)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) ps[v & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, negm));
+        for (int v = 0; v < 16; ++v) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, negm));
+          ps[v & 3] = (kb == 0 && v < 4) ? e : ps[v & 3] + e;
+        }
       const float tsum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
       exact = __ballot(!(tsum < 65536.0f)) != 0;
       if (!exact) l = l + tsum;
@@ -180,11 +183,14 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
       const float m_new = fmaxf(m, mx);
       const float corr = __builtin_amdgcn_exp2f((m - m_new) * c);  // m = -inf on the first tile: corr = 0
       const float neg = 0.0f - m_new * c;
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float ps[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) ps[v & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, neg));
+        for (int v = 0; v < 16; ++v) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[kb][v], c, neg));
+          ps[v & 3] = (kb == 0 && v < 4) ? e : ps[v & 3] + e;
+        }
       l = l * corr + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
       m = m_new;
       negm = m == -INFINITY ? 0.0f : neg;  // a row with no visible key yet keeps m = -inf
