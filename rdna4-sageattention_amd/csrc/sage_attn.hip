@@ -16,7 +16,12 @@
 // F = c + S * 2^-26 and needs no conversion; nk = -(cl * m_new) - fp32(c * ct), so F * ct + nk equals
 // S * ct - cl * m_new up to the rounding of nk.  Those kernels keep cl scaled by 2^26 and m by 2^-26 (powers of
 // two: every product and difference of the math above is the same bits, scaled).  Head dim 256 reaches |S| = 4,129,024, outside that binade, so its
-// accumulators start at 0 and F = fp32(S) (v_cvt_f32_i32), nk = -(cl * m_new): the reference's arithmetic.
+// accumulators start at 0 and F = fp32(S) (v_cvt_f32_i32), nk = -(cl * m_new): the reference's arithmetic.  The
+// rounding of fp32(c * ct) grows with the input scale; a wave whose scales are large enough for it to matter reads
+// F - c = S * 2^-26 (exact) with nk = -(cl * m_new) instead (the `wide` test, once per work unit).
+// Passes.  Once every row of a wave has a max, a tile first runs without the block maxima: p with the current m,
+// kept when every lane's sum of 16 probabilities of each block stays below 2^7.5 (then no row's max can move), else
+// redone exactly (the maxima, the lazy-rescale decisions above, and a second pass when block 1 rescales).
 //
 // gfx950 mapping.  A workgroup owns 128 query rows (4 waves x 32) of one (batch, head) and walks the KV sequence
 // in 64-key tiles staged in LDS by direct global -> LDS loads (three buffers at head dims up to 128, the loads of the
