@@ -133,9 +133,9 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
   // One tile: S^T from the LDS buffer, the MASKED body clears keys past Skv and (causal) past the row's diagonal.
   // The two bodies sit in two loops (tiles before t_mask need no mask for any row of the wave): with the mask test
   // in one loop the compiler turns the masking into compares and selects on every tile.
-  auto tile = [&](int t, auto masked) {
+  auto tile = [&](int t, auto masked, auto buf) {
     constexpr bool MASKED = decltype(masked)::value;
-    const uint8_t* kt = smem[t & 1];
+    const uint8_t* kt = smem[buf];  // a compile-time buffer in the mask-free loop: the LDS reads take it as an offset
     v16f s0 = {}, s1 = {};
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
@@ -209,13 +209,23 @@ __global__ __launch_bounds__(LSE_THREADS, 2) void lse_kernel(const uint16_t* __r
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   int t = 0;
-  for (; t < t_mask; ++t) {
-    if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
-    tile(t, std::false_type{});
+  // the mask-free tiles in pairs (t even: buffer 0, then 1), so that each body's buffer is a constant
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  for (; t + 1 < t_mask; t += 2) {
+    issue(t + 1, 1);
+    tile(t, std::false_type{}, B0{});
+    if (t + 2 < ntiles) issue(t + 2, 0);
+    tile(t + 1, std::false_type{}, B1{});
+  }
+  if (t < t_mask) {
+    if (t + 1 < ntiles) issue(t + 1, 1);
+    tile(t, std::false_type{}, B0{});
+    ++t;
   }
   for (; t < ntiles; ++t) {
     if (t + 1 < ntiles) issue(t + 1, (t + 1) & 1);
-    tile(t, std::true_type{});
+    tile(t, std::true_type{}, t & 1);
   }
   const float lt = add_xor32_f32(l);
   if (qvalid && hf == 0) lse[(int64_t)bh * Sq + qrow] = 0.69314718055994531f * (m * c + __log2f(lt));
