@@ -35,7 +35,9 @@ What each function restates (paths relative to the reference checkout):
                         fma(c + S * 2^-26, ct * 2^26, nk) form (c = fp32(1 / (2 pi))), which differs from the
                         reference's S * ct - cl * m by the rounding of nk (at most 1.5 * ct: S moved by less than
                         2 units, far below the int8 quantization error of S and the E4M3 step of p); head dim 256
-                        uses fma(fp32(S), ct, -cl * m), the reference's own form.
+                        uses fma(fp32(S), ct, -cl * m), the reference's own form, and so do 32-row groups whose
+                        scales are large enough for the seeded form's rounding to matter (``wide_rows``: the
+                        kernel's own rule, pinned by the single-key bound at scale 100 in tests/test_oracle.py).
                         Bottom-right causal for any q_len / kv_len: query i sees keys j <= i + kv_len - q_len; a
                         query that sees no key (q_len > kv_len) gives a 0 row (the gfx950 convention; the reference
                         sends such calls to SDPA, so this case has no reference value).
