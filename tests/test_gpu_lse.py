@@ -149,3 +149,15 @@ def test_random_lse_vs_float64(dev, case):
     assert got.shape == (B, H, Sq) and np.isfinite(got).all()
     ref = orc.lse_reference(_hnd(q, layout), _hnd(k, layout), causal=causal, sm_scale=sm)
     assert np.abs(got - ref).max() <= 1e-4 + 1e-6 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_lse_large_scales(dev, causal):
+    """Inputs scaled by 100 (logits ~10^5): the running max moves rarely and by much; the float64 bound holds."""
+    g = torch.Generator().manual_seed(77 + causal)
+    q = (torch.randn(1, 2, 300, 128, generator=g) * 100).to(torch.bfloat16)
+    k = (torch.randn(1, 2, 700, 128, generator=g) * 100).to(torch.bfloat16)
+    got = cdna4_sage.lse(q.to(dev), k.to(dev), "HND", None, causal).cpu().numpy()
+    ref = orc.lse_reference(_hnd(q, "HND"), _hnd(k, "HND"), causal=causal)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= 1e-4 + 1e-6 * np.abs(ref).max()
