@@ -41,13 +41,11 @@ def device_arch(device: torch.device) -> str:
 def _bsh(t: torch.Tensor, layout: str):
     """(batch, seq, head) element strides.  The quantizers load 16-byte vectors, so the base must be 16-byte aligned
     and the strides multiples of 8 elements; anything else is made contiguous (reference: _attention.py:59-67)."""
-    if t.stride(-1) != 1 or t.data_ptr() % 16:
+    s = t.stride()
+    if s[3] != 1 or t.data_ptr() % 16 or s[0] % 8 or s[1] % 8 or s[2] % 8:
         t = t.contiguous()
-    st = (t.stride(0), t.stride(2), t.stride(1)) if layout == "HND" else (t.stride(0), t.stride(1), t.stride(2))
-    if any(s % 8 for s in st):
-        t = t.contiguous()
-        st = (t.stride(0), t.stride(2), t.stride(1)) if layout == "HND" else (t.stride(0), t.stride(1), t.stride(2))
-    return t, st
+        s = t.stride()
+    return t, ((s[0], s[2], s[1]) if layout == "HND" else s[:3])
 
 
 def check_supported(q, k, v, layout, is_causal=False):
@@ -145,8 +143,9 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False, attn_mask=N
     q, sq_ = _bsh(q, layout)
     k, sk_ = _bsh(k, layout)
     v, sv_ = _bsh(v, layout)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    di = dev.index if dev.index is not None else torch.cuda.current_device()
+    cur = torch.cuda.current_device()
+    di = cur if dev.index is None else dev.index
+    stream = torch._C._cuda_getCurrentRawStream(di)
     causal = bool(is_causal)
     offs, total, ws_bytes, _, _ = _forward_layout(di, B, H, Hkv, Sq, Skv, D, causal,
                                                   None if attn_mask is None else (mcode, *mstr))
@@ -163,7 +162,7 @@ def attention(q, k, v, layout="HND", sm_scale=None, is_causal=False, attn_mask=N
         args = ("sage_forward", _ptr(q), *sq_, _ptr(k), *sk_, _ptr(v), *sv_, _ptr(out), *_out_strides(out),
                 B, H, Hkv, Sq, Skv, D, dt, int(causal), qs_fold_factor(sm_scale, D),
                 q8, qs, k8, ks, v8t, vs, ws, ws_bytes, stream)
-    if di == torch.cuda.current_device():
+    if di == cur:
         _capi.call(*args)
     else:
         with torch.cuda.device(dev):
@@ -196,7 +195,7 @@ def _forward_layout(di: int, B: int, H: int, Hkv: int, Sq: int, Skv: int, D: int
 
 def _out_strides(out: torch.Tensor):
     # out is (B, Sq, H, D): (batch, seq, head) element strides
-    return out.stride(0), out.stride(1), out.stride(2)
+    return out.stride()[:3]
 
 
 def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
