@@ -192,7 +192,7 @@ int sage_mask_workspace(int B, int H, int Hkv, int Sq, int Skv, int D, int causa
 /*
  * sage_forward with an attention mask: the same quantization and quantized attention, with the mask applied to the
  * scores (bool: masked keys at -inf; float: the values added, ANDed / combined with the bottom-right causal mask when
- * causal is set).  A query row that sees no key is written as 0 (torch SDPA gives NaN there).  Same arguments as
+ * causal is set).  A query row that sees no key is written as 0 (as torch 2.10's SDPA writes it, on gfx950 and on the CPU).  Same arguments as
  * sage_forward plus the mask; workspace: sage_mask_workspace bytes, 256-byte aligned (required).  Replaces, for
  * these masks, the torch SDPA call of src/rdna4_sage/__init__.py:44-56 (`_sdpa`) that the reference makes for every
  * call with an attn_mask.

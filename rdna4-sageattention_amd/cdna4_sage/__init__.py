@@ -118,7 +118,7 @@ def sageattn(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, attn_
     """Drop-in for sageattention.sageattn.  Uses the gfx950 kernel when it applies and pays off, torch SDPA otherwise
     (masks of another dtype, causal with q_len > kv_len, unsupported shapes or GPUs, small problems).  Causal attention
     is bottom-right aligned as in SageAttention / FlashAttention.  A bool attn_mask, or an additive one of q's dtype,
-    runs on the kernel (a query row that sees no key gives 0 there, NaN in SDPA).  Extra SageAttention kwargs are
+    runs on the kernel (a query row that sees no key gives 0 there, as torch SDPA gives).  Extra SageAttention kwargs are
     ignored."""
     if return_lse:
         raise NotImplementedError("cdna4_sage: return_lse is not supported here; use sageattention.sageattn")

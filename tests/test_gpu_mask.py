@@ -157,8 +157,9 @@ def test_fully_masked_rows_and_tiles_give_zero(dev):
 
 
 def test_sageattn_routes_bool_masks_to_the_kernel(dev, monkeypatch):
-    """sageattn (and sageattention.sageattn through kwargs) runs boolean masks on the kernel above the routing
-    threshold, float masks on SDPA; CDNA4_SAGE_NATIVE_MASK=0 restores the reference's SDPA routing."""
+    """sageattn (and sageattention.sageattn through kwargs) runs boolean masks, and additive ones of the inputs'
+    dtype, on the kernel above the routing threshold; CDNA4_SAGE_NATIVE_MASK=0 restores the reference's SDPA
+    routing."""
     import sageattention
     monkeypatch.setattr(cdna4_sage, "MIN_WORK", 0)      # 8 x 1024 x 1024 is below the default threshold
     q, k, v = (t.to(dev) for t in _inputs(1, 8, 8, 1024, 1024, 64, torch.bfloat16, "HND", seed=7))
@@ -171,7 +172,7 @@ def test_sageattn_routes_bool_masks_to_the_kernel(dev, monkeypatch):
     fmask = torch.zeros(1, 1, 1, 1024, device=dev, dtype=torch.bfloat16)
     fmask[..., 900:] = float("-inf")
     assert torch.equal(cdna4_sage.sageattn(q, k, v, attn_mask=fmask), kern)   # the same mask as an additive one
-    # a query row that sees no key: 0 on the kernel route, torch SDPA's own output (NaN for its math path) with
+    # a query row that sees no key: 0 on the kernel route, and 0 from torch SDPA (this torch, bool mask, bf16) on
     # the reference's routing; every other row is the same on both routes as above
     rowmask = torch.ones(1, 1, 1024, 1024, dtype=torch.bool, device=dev)
     rowmask[..., 7, :] = False
@@ -183,6 +184,7 @@ def test_sageattn_routes_bool_masks_to_the_kernel(dev, monkeypatch):
     ref_rows = cdna4_sage._torch_sdpa(q, k, v, attn_mask=rowmask)
     assert torch.equal(sdpa_rows.isnan(), ref_rows.isnan())
     assert torch.equal(torch.nan_to_num(sdpa_rows), torch.nan_to_num(ref_rows))
+    assert torch.equal(sdpa_rows[:, :, 7], kern_rows[:, :, 7])     # both routes: 0
 
 
 def _alibi(H, Sq, Skv, slope=0.03):
