@@ -40,10 +40,11 @@ def device_arch(device: torch.device) -> str:
 
 def _bsh(t: torch.Tensor, layout: str):
     """(batch, seq, head) element strides.  The quantizers load 16-byte vectors, so the base must be 16-byte aligned
-    and the strides multiples of 8 elements; anything else is made contiguous (reference: _attention.py:59-67)."""
+    and the strides multiples of 8 elements; anything else is copied to a new contiguous tensor (reference:
+    _attention.py:59-67).  .contiguous() alone would keep an already contiguous tensor on a misaligned base."""
     s = t.stride()
     if s[3] != 1 or t.data_ptr() % 16 or s[0] % 8 or s[1] % 8 or s[2] % 8:
-        t = t.contiguous()
+        t = t.clone(memory_format=torch.contiguous_format)
         s = t.stride()
     return t, ((s[0], s[2], s[1]) if layout == "HND" else s[:3])
 
@@ -237,9 +238,9 @@ def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
 
 def _packed(t: torch.Tensor):
     """(token, head) element strides of a packed [tokens, heads, D] tensor, made contiguous when the kernels cannot
-    load it as 16-byte vectors."""
+    load it as 16-byte vectors (a new tensor: .contiguous() keeps a contiguous one on a misaligned base)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 or t.stride(0) % 8 or t.stride(1) % 8:
-        t = t.contiguous()
+        t = t.clone(memory_format=torch.contiguous_format)
     return t, (t.stride(0), t.stride(1))
 
 

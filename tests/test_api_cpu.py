@@ -301,3 +301,31 @@ def test_qs_fold_factor_maps_non_positive_scales_to_the_default():
     for sm, d in ((0.05, 128), (0.3, 64), (1.0, 96)):
         assert qs_fold_factor(sm, d) == pytest.approx(sm * d ** 0.5, rel=1e-12)
         assert np.float32(qs_fold_factor(sm, d)) == orc.qs_fold_factor(sm, d)
+
+
+def test_bsh_strides_and_the_copy_rule():
+    """(batch, seq, head) element strides handed to the quantizers (reference: src/rdna4_sage/_attention.py:59-67):
+    views whose strides are multiples of 8 elements and whose base is 16-byte aligned pass through uncopied, in
+    both layouts; anything else is made contiguous first."""
+    from cdna4_sage._attention import _bsh
+    x = torch.zeros(2, 3, 40, 64, dtype=torch.bfloat16)                  # HND [B, H, S, D]
+    t, st = _bsh(x, "HND")
+    assert t.data_ptr() == x.data_ptr() and st == (3 * 40 * 64, 64, 40 * 64)
+    t, st = _bsh(x, "NHD")                                                # read as [B, S, H, D]
+    assert t.data_ptr() == x.data_ptr() and st == (3 * 40 * 64, 40 * 64, 64)
+    y = x.transpose(1, 2)                                                 # NHD view of the HND tensor
+    t, st = _bsh(y, "NHD")
+    assert t.data_ptr() == x.data_ptr() and st == (3 * 40 * 64, 64, 40 * 64)
+    z = torch.zeros(2, 3, 40, 72, dtype=torch.bfloat16)[..., :64]        # row stride 72: a multiple of 8, kept
+    t, st = _bsh(z, "HND")
+    assert t.data_ptr() == z.data_ptr() and st == (3 * 40 * 72, 72, 40 * 72)
+    w = torch.zeros(2, 3, 40, 68, dtype=torch.bfloat16)[..., :64]        # row stride 68: copied
+    t, st = _bsh(w, "HND")
+    assert t.is_contiguous() and st == (3 * 40 * 64, 64, 40 * 64)
+    u = torch.zeros(2 * 3 * 40 * 64 + 8, dtype=torch.bfloat16)[4:4 + 2 * 3 * 40 * 64].view(2, 3, 40, 64)
+    assert u.data_ptr() % 16 == 8
+    t, st = _bsh(u, "HND")                                                # 8-byte aligned base: copied
+    assert t.data_ptr() != u.data_ptr() and t.data_ptr() % 16 == 0 and st == (3 * 40 * 64, 64, 40 * 64)
+    v = x[..., ::2]                                                       # channel stride 2: copied
+    t, st = _bsh(v, "HND")
+    assert t.is_contiguous() and st == (3 * 40 * 32, 32, 40 * 32)

@@ -205,6 +205,32 @@ def test_varlen(dev):
         assert cos(out[s].transpose(0, 1)[None], ref) > COS, i
 
 
+def _misaligned(t):
+    """A contiguous copy of t whose base sits 4 elements (8 bytes) past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 8, device=t.device, dtype=t.dtype)
+    u = buf[4:4 + t.numel()].view(t.shape)
+    u.copy_(t)
+    assert u.is_contiguous() and u.data_ptr() % 16 == 8
+    return u
+
+
+def test_misaligned_contiguous_inputs(dev):
+    """Contiguous inputs on a base that is not 16-byte aligned (e.g. a view 4 elements into a buffer) are copied to
+    an aligned tensor before the C call: the same bits as the aligned inputs, on the dense, LSE and varlen paths."""
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (rand((1, 4, 1000, 128), torch.bfloat16, g, dev) for _ in range(3))
+    want = cdna4_sage.attention(q, k, v, "HND", is_causal=True)
+    got = cdna4_sage.attention(_misaligned(q), _misaligned(k), _misaligned(v), "HND", is_causal=True)
+    assert torch.equal(got, want)
+    assert torch.equal(cdna4_sage.lse(_misaligned(q), _misaligned(k), "HND", None, True),
+                       cdna4_sage.lse(q, k, "HND", None, True))
+    cu = torch.tensor([0, 700, 1000], dtype=torch.int32, device=dev)
+    qp, kp, vp = (t[0].transpose(0, 1).contiguous() for t in (q, k, v))     # packed [tokens, heads, D]
+    want = cdna4_sage.attention_varlen(qp, kp, vp, cu, cu, 700, 700)
+    got = cdna4_sage.attention_varlen(_misaligned(qp), _misaligned(kp), _misaligned(vp), cu, cu, 700, 700)
+    assert torch.equal(got, want)
+
+
 def test_concurrent_streams_do_not_share_state(dev):
     """Entry points take their arguments by value: two streams running different problems at once give the same
     results as running them one after the other (the reference packs kernargs into one buffer per kernel)."""
