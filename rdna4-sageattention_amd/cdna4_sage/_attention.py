@@ -69,10 +69,10 @@ def check_supported(q, k, v, layout, is_causal=False):
     h_ax, s_ax = (1, 2) if layout == "HND" else (2, 1)
     if q.shape[0] != k.shape[0] or k.shape[0] != v.shape[0] or k.shape[h_ax] != v.shape[h_ax] or k.shape[s_ax] != v.shape[s_ax]:
         raise Unsupported("q/k/v batch, k/v heads and k/v lengths must match")
+    if max(q.numel(), k.numel()) > _I32_MAX or k.numel() == 0 or q.numel() == 0:
+        raise Unsupported("tensor too large for 32-bit indexing or empty")
     if q.shape[h_ax] % k.shape[h_ax]:
         raise Unsupported(f"heads {q.shape[h_ax]} not a multiple of kv heads {k.shape[h_ax]}")
-    if max(q.numel(), k.numel()) > _I32_MAX or k.shape[s_ax] == 0 or q.shape[s_ax] == 0:
-        raise Unsupported("tensor too large for 32-bit indexing or empty")
     if is_causal and q.shape[s_ax] > k.shape[s_ax]:
         raise Unsupported("causal attention needs q_len <= kv_len (bottom-right aligned)")
 

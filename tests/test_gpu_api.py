@@ -231,6 +231,21 @@ def test_misaligned_contiguous_inputs(dev):
     assert torch.equal(got, want)
 
 
+def test_empty_inputs(dev):
+    """An empty batch, no heads or no tokens: Unsupported from the kernel API (no C call); the routed API returns the
+    empty output without calling torch SDPA, which raises for an empty batch on gfx950 and stops the process with
+    SIGFPE for zero heads."""
+    for shape_q, shape_kv in (((0, 4, 256, 128), (0, 4, 256, 128)), ((1, 0, 256, 128), (1, 0, 256, 128)),
+                              ((1, 4, 0, 128), (1, 4, 256, 128)), ((1, 4, 256, 128), (1, 4, 0, 128))):
+        q = torch.zeros(shape_q, device=dev, dtype=torch.bfloat16)
+        k = torch.zeros(shape_kv, device=dev, dtype=torch.bfloat16)
+        with pytest.raises(cdna4_sage.Unsupported):
+            cdna4_sage.attention(q, k, k, "HND")
+        if q.numel() == 0:
+            out = sageattention.sageattn(q, k, k)
+            assert out.shape == q.shape and out.dtype == q.dtype and out.device == q.device
+
+
 def test_concurrent_streams_do_not_share_state(dev):
     """Entry points take their arguments by value: two streams running different problems at once give the same
     results as running them one after the other (the reference packs kernargs into one buffer per kernel)."""
