@@ -85,9 +85,9 @@ def attention(q, k, v, tensor_layout="HND", sm_scale=None, is_causal=False, attn
 
 
 def _sdpa(q, k, v, tensor_layout, is_causal, sm_scale, attn_mask):
-    if q.is_cuda and q.numel() == 0:
+    if q.numel() == 0:
         # no query rows (empty batch, no heads or no tokens): the empty output itself.  torch SDPA raises for an
-        # empty batch on the GPU and stops the process with SIGFPE for zero heads (torch 2.10, gfx950).
+        # empty batch on the GPU and stops the process with SIGFPE for zero heads (torch 2.10, CPU and gfx950).
         return q.new_empty(tuple(q.shape[:-1]) + (v.shape[-1],))
     if tensor_layout == "NHD":
         q, k, v = (t.transpose(1, 2) for t in (q, k, v))

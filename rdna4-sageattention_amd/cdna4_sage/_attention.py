@@ -219,7 +219,7 @@ def lse(q, k, layout="HND", sm_scale=None, is_causal=False):
         Skv, Hkv = k.shape[1], k.shape[2]
     if D not in LSE_HEAD_DIMS or k.shape[-1] != D or k.shape[0] != B or Hkv == 0 or H % Hkv:
         raise Unsupported("head_dim / head counts")
-    if Sq == 0 or Skv == 0 or max(q.numel(), k.numel()) > _I32_MAX:
+    if q.numel() == 0 or k.numel() == 0 or max(q.numel(), k.numel()) > _I32_MAX:
         raise Unsupported("empty or too large")
     if is_causal and Sq > Skv:
         raise Unsupported("causal LSE needs q_len <= kv_len")

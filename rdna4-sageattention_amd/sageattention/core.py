@@ -37,6 +37,8 @@ def _lse(q, k, tensor_layout, is_causal, sm_scale):
     q, k = _as_hnd(q, tensor_layout), _as_hnd(k, tensor_layout)
     B, H, Sq, D = q.shape
     Hkv, Skv = k.shape[1], k.shape[2]
+    if q.numel() == 0 or Hkv == 0:
+        return torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)   # no query rows: nothing to compute
     rep = H // Hkv
     scale = D ** -0.5 if sm_scale is None else sm_scale
     out = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)

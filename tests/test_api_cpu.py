@@ -329,3 +329,13 @@ def test_bsh_strides_and_the_copy_rule():
     v = x[..., ::2]                                                       # channel stride 2: copied
     t, st = _bsh(v, "HND")
     assert t.is_contiguous() and st == (3 * 40 * 32, 32, 40 * 32)
+
+
+def test_return_lse_with_empty_inputs():
+    """No query rows (empty batch, no heads, no tokens): the output and the logsumexp come back empty, with
+    [batch, heads, q_len] for the latter."""
+    for shape in ((0, 2, 16, 64), (1, 0, 16, 64), (1, 2, 0, 64)):
+        q = torch.zeros(shape)
+        k = torch.zeros(shape[:2] + (16, 64))
+        out, lse = sageattention.sageattn(q, k, k, return_lse=True)
+        assert out.shape == q.shape and lse.shape == shape[:3] and lse.dtype == torch.float32
