@@ -12,6 +12,10 @@ Prints ONE JSON line on stdout:
 Everything else (per-kernel times, quantizer GB/s, torch SDPA bf16 on the same GPU) goes to the "detail" object.
 
 usage: python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--no-cpu-baseline] [--config 2]
+       python bench.py --models [name ...]      (the reference's model-shape table; one JSON line with every row)
+
+--config takes a configuration of cdna4_sage.configs: 2 (default), 3, 4, 5a, 5b, 1, lumina (head dim 96),
+auraflow (head dim 256).
 
 Order: 0.3 s of forward calls take the GPU clock out of its idle state (in which the first ~25 ms of calls run ~15%
 slower), then the per-kernel measurements run, then exactly --warmup untimed steps and the --steps timed ones (mean
@@ -108,7 +112,101 @@ def cpu_baseline(cfg, target_s=15.0):
 
 
 PROFILE_STEMS = {"2": "flux_config2", "3": "wan14b_config3", "4": "hunyuan_config4", "5a": "causal_gqa_config5a",
-                 "5b": "causal_gqa_d64_config5b"}
+                 "5b": "causal_gqa_d64_config5b", "lumina": "neta_lumina_d96", "auraflow": "auraflow_d256"}
+
+# The model shapes of the reference's benchmark (tests/bench_models.py:15-42): name, B, Sq, Skv, H, D, layout, dtype
+# name, causal.  Timed with its method (3 warm-ups, median of 10 calls each followed by a synchronisation,
+# tests/bench_models.py:45-53) on random N(0, 1) inputs: torch SDPA, the kernel-forced call, the routed call.
+MODEL_SHAPES = [
+    ("SD1.5 512 (d40->sdpa)", 2, 4096, 4096, 8, 40, "NHD", "f16", False),
+    ("SDXL 1024 lvl1 self", 2, 4096, 4096, 10, 64, "NHD", "f16", False),
+    ("SDXL 1024 lvl2 self", 2, 1024, 1024, 20, 64, "NHD", "f16", False),
+    ("SDXL 1024 lvl1 cross77", 2, 4096, 77, 10, 64, "NHD", "f16", False),
+    ("SD3.5L joint", 2, 4250, 4250, 38, 64, "NHD", "f16", False),
+    ("Flux 1024 joint", 1, 4352, 4352, 24, 128, "HND", "bf16", False),
+    ("Flux 768 joint", 1, 2560, 2560, 24, 128, "HND", "bf16", False),
+    ("Flux 512 joint", 1, 1280, 1280, 24, 128, "HND", "bf16", False),
+    ("Flux.2 1024 joint", 1, 4608, 4608, 48, 128, "HND", "bf16", False),
+    ("Qwen-Image 1328 joint", 1, 6989, 6989, 24, 128, "HND", "bf16", False),
+    ("HiDream 1024 joint", 1, 4480, 4480, 20, 128, "NHD", "bf16", False),
+    ("Neta Lumina 1024", 1, 4352, 4352, 24, 96, "HND", "bf16", False),
+    ("Anima 1024 self", 2, 4096, 4096, 16, 128, "HND", "bf16", False),
+    ("Anima 1024 cross512", 2, 4096, 512, 16, 128, "HND", "bf16", False),
+    ("Wan1.3B 480p self", 1, 32760, 32760, 12, 128, "NHD", "f16", False),
+    ("Wan1.3B 480p cross512", 1, 32760, 512, 12, 128, "NHD", "f16", False),
+    ("Wan14B 480p self", 1, 32760, 32760, 40, 128, "NHD", "f16", False),
+    ("Wan2.2-5B 704p self", 1, 27280, 27280, 24, 128, "NHD", "f16", False),
+    ("HunyuanVideo 544p", 1, 67320, 67320, 24, 128, "HND", "bf16", False),
+    ("LTXV-2B 768x512x97", 1, 4992, 4992, 32, 64, "NHD", "bf16", False),
+    ("LTXV-2B cross128", 1, 4992, 128, 32, 64, "NHD", "bf16", False),
+    ("CogVideoX-5B joint", 1, 17776, 17776, 48, 64, "NHD", "bf16", False),
+    ("AuraFlow 1024 joint d256", 2, 4360, 4360, 12, 256, "HND", "f16", False),
+    ("causal d128 4k", 1, 4096, 4096, 32, 128, "HND", "bf16", True),
+    ("causal d128 16k", 1, 16384, 16384, 32, 128, "HND", "bf16", True),
+    ("causal d64 8k", 1, 8192, 8192, 32, 64, "HND", "bf16", True),
+]
+
+
+def median_synced_ms(fn, n=10):
+    """The reference's per-call time: 3 warm-up calls, then the median of n calls each followed by a sync."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(ts)
+
+
+def bench_models(only):
+    """Every shape of MODEL_SHAPES (or those whose name contains one of `only`): SDPA, kernel-forced and routed
+    ms per call, and the kernel's TOPS (4 * B * H * pairs * D per call, pairs = Sq * Skv or its causal half)."""
+    import torch
+    import torch.nn.functional as F
+
+    import cdna4_sage
+    import sageattention
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    dts = {"bf16": torch.bfloat16, "f16": torch.float16}
+    rows = []
+    log(f"{'shape':26s} {'sdpa ms':>9s} {'kernel ms':>10s} {'speedup':>8s} {'routed ms':>10s} {'TOPS':>7s}  route")
+    for name, B, Sq, Skv, H, D, layout, dt, causal in MODEL_SHAPES:
+        if only and not any(o.lower() in name.lower() for o in only):
+            continue
+        g = torch.Generator().manual_seed(len(rows))
+        shp = (lambda s: (B, H, s, D)) if layout == "HND" else (lambda s: (B, s, H, D))  # noqa: E731
+        q, k, v = (torch.randn(shp(s), generator=g).to(dts[dt]).to(dev) for s in (Sq, Skv, Skv))
+        hnd = (lambda x: x) if layout == "HND" else (lambda x: x.transpose(1, 2))  # noqa: E731
+        t_sdpa = median_synced_ms(lambda: F.scaled_dot_product_attention(hnd(q), hnd(k), hnd(v), is_causal=causal))
+        try:
+            t_kern = median_synced_ms(lambda: cdna4_sage.attention(q, k, v, layout, is_causal=causal))
+        except cdna4_sage.Unsupported:
+            t_kern = None
+        t_route = median_synced_ms(lambda: sageattention.sageattn(q, k, v, tensor_layout=layout, is_causal=causal))
+        routed = t_kern is not None and cdna4_sage._worth_it(q, k, layout, causal)
+        pairs = Sq * (Sq + 1) // 2 if causal and Sq == Skv else Sq * Skv
+        tops = 4 * B * H * pairs * D / (t_kern * 1e-3) / 1e12 if t_kern else None
+        row = {"shape": name, "B": B, "Sq": Sq, "Skv": Skv, "H": H, "D": D, "layout": layout, "dtype": dt,
+               "causal": causal, "sdpa_ms": round(t_sdpa, 4), "kernel_ms": None if t_kern is None else round(t_kern, 4),
+               "speedup": None if t_kern is None else round(t_sdpa / t_kern, 3), "routed_ms": round(t_route, 4),
+               "kernel_TOPS": None if tops is None else round(tops, 1), "route": "kernel" if routed else "sdpa"}
+        rows.append(row)
+        log(f"{name:26s} {t_sdpa:9.3f} {t_kern if t_kern else float('nan'):10.3f} "
+            f"{(t_sdpa / t_kern) if t_kern else float('nan'):7.2f}x {t_route:10.3f} {tops or float('nan'):7.1f}  "
+            f"{row['route']}")
+        del q, k, v
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "per-call ms of the reference's model shapes (tests/bench_models.py), SDPA vs "
+                                "kernel vs routed", "unit": "ms", "higher_is_better": False, "n_gpus": 1,
+                      "method": "median of 10 synced calls after 3 warm-ups", "data": "synthetic N(0,1)",
+                      "device": torch.cuda.get_device_name(dev), "shapes": rows}), flush=True)
 
 
 def profiled_traffic(cfg_key):
@@ -136,11 +234,16 @@ def main():
                     help="also time the attention with every query tile whole (no workspace)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (calibrates rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--models", nargs="*", default=None,
+                    help="time the reference's model shapes instead (all, or those whose name contains an argument)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this path runs on one GPU; --gpus {args.gpus} is not supported (each call is a single-device "
               "op on one GPU; sharding heads or sequences over several GPUs is not built)", file=sys.stderr)
         sys.exit(2)
+    if args.models is not None:
+        bench_models(args.models)
+        return
 
     import torch
     import torch.nn.functional as F

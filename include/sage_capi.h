@@ -17,7 +17,7 @@
  *    pointers 16-byte aligned and strides multiples of 8 elements (the quantizers load 16-byte vectors).
  *  - dtype: SAGE_DTYPE_BF16 or SAGE_DTYPE_F16; head_dim D = 64, 96, 128 or 256 (kernel_build/build_kernels.py:26).
  *    Q and K are rotated by the unnormalised Hadamard matrix of RB = min(D, 128) channels (block-diagonal for 256);
- *    D = 96 is not rotated (kernel_build/build_kernels.py:36-37, sage_quant.py:18-30).
+ *    D = 96 is not rotated (kernel_build/build_kernels.py:40-41, :102-104; sage_quant.py:18-30).
  *
  * Intermediate layouts (device memory, all contiguous; DL = sage_layout_dim(D): D, or 128 for D = 96 whose rows are
  * zero-padded; the attention kernel reads them as 128-channel tiles):
@@ -212,7 +212,9 @@ int sage_forward_masked(const void* q, int64_t qsb, int64_t qss, int64_t qsh, co
  * that forbid it).  No counterpart in the reference.  A shape whose intermediates and workspace exceed the array
  * returns SAGE_ERR_INVALID (128 MiB holds e.g. [1, 24, 4608, 128], 69 MB, and [2, 32/8, 8192, 128], 103 MB).  Every
  * call on a GPU shares that GPU's array: calls that overlap on one GPU (different streams or threads without
- * ordering) race; calls ordered on one stream do not.  Nothing in the array needs clearing between calls.
+ * ordering) race and give wrong outputs without an error; calls ordered on one stream do not.  Nothing in the array
+ * needs clearing between calls.  The first call on each GPU looks up the array's address (hipGetSymbolAddress, which
+ * may load the code object): make one eager call per GPU before capturing calls into a HIP graph.
  */
 #define SAGE_NOALLOC_SCRATCH_BYTES (128ll << 20)
 int sage_forward_noalloc(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const void* k, int64_t ksb,

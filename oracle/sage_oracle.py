@@ -143,7 +143,8 @@ def fwht_rows(x: np.ndarray) -> np.ndarray:
 
 def rotation_block(d: int) -> int:
     """Channels of one Hadamard block for head_dim d: min(d, 128) for powers of two (kernel_build/build_kernels.py:27,
-    :36-37, HADAMARD_MAX = 128: block-diagonal for d = 256, sage_quant.py:18-30), 0 (no rotation) otherwise (d = 96)."""
+    HADAMARD_MAX = 128; rotates() :40-41 applied at :102-104: block-diagonal for d = 256, sage_quant.py:18-30), 0 (no
+    rotation) otherwise (d = 96)."""
     return min(d, 128) if d & (d - 1) == 0 else 0
 
 
@@ -278,7 +279,7 @@ def logit_scale_base(d: int) -> np.float32:
 
 def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n: int = 32,
               out_dtype: str = "bf16", threshold: float = RESCALE_THRESHOLD, return_stats: bool = False,
-              kv_split=None, attn_mask=None, q_rows=None, seq_q=None):
+              kv_split=None, attn_mask=None, q_rows=None, seq_q=None, also_unsplit=False):
     """Quantized attention as the reference kernel computes it.
 
     q8 [B, H, Sq, D] int8, qs [B, H, Sq] f32, k8 [B, Hkv, Sp, D] int8, ks [B, Hkv, Sp/32] f32,
@@ -288,7 +289,9 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     ``kv_split = (chunks, rows)``, rows a bool array [B, H, Sq], emulates the gfx950 kernel's split tiles (no
     counterpart in the reference): for those rows the keys run as ``chunks`` contiguous ranges (range c = the
     kernel's 64-key tiles [c * n // chunks, (c + 1) * n // chunks), n = ceil(seq_kv / 64), whatever ``block_n``),
-    each with its own online softmax from m = -inf, stored as
+    each with its own online softmax, l = 0, O = 0 and m = -inf, except that a range starting after the first 64-key
+    kernel tile that any row of its 128-row block sees starts from the running max that the one-walk softmax has
+    after that tile (the kernel's seed; without a mask that is tile 0), stored as
     (m_c, l_c, fp16(O_c / l_c)) and merged with M = max m_c, W_c = exp2((m_c - M) * cl) * l_c, L = sum W_c,
     O = sum W_c * fp16(O_c / l_c) (float32, chunk order), then the usual epilogue with L.  A range in which a row
     sees no key (l_c = 0, m_c = -inf) stores 0 and weighs 0.
@@ -303,7 +306,10 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
 
     ``q_rows`` (int array, with ``seq_q``): the query axis of q8 / qs holds only these rows of a query sequence of
     length seq_q (a sample of a long problem; the bottom-right causal mask and ``kv_split`` rows refer to these
-    positions).  Not combined with ``attn_mask``."""
+    positions).  Not combined with ``attn_mask``.
+
+    ``also_unsplit``: return ``(out, out_unsplit)``, where ``out_unsplit`` walks every key of the split rows in one
+    online softmax, as the reference does (kernel_build/make_sage_r2.py:141-253); it is computed on the way."""
     B, H, Sq, D = q8.shape
     Hkv = k8.shape[1]
     assert block_n % KV_BLOCK == 0 and KERNEL_TILE % block_n == 0 and H % Hkv == 0
@@ -330,11 +336,26 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
     wide = wide_rows(cl, ks, seq_kv, qpos[0], hk) if seeded(D) else None
     o, m, l = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, n_tiles, attn_mask, qpos,
                               wide)
+
+    def epilogue(o, l):
+        with np.errstate(divide="ignore"):
+            inv = np.where(l > 0, (F32(1.0 / 448.0) / l).astype(F32), F32(0.0)).astype(F32)   # no visible key: 0
+        res = ((o * inv[..., None]).astype(F32) * vs[:, hk][:, :, None, :].astype(F32)).astype(F32)
+        return round_output(res, out_dtype)
+
+    unsplit = epilogue(o, l) if also_unsplit else None
     if kv_split is not None:
         chunks, rows = kv_split
-        parts = [_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold,
-                                 *krange(c, chunks), attn_mask, qpos, wide)
-                 for c in range(chunks)]
+        # the kernel's seed: a range that starts after the first kernel tile its 128-row block visits starts from the
+        # walk's running max after that tile, instead of from -inf (no mask: tile 0; the kernel splits only
+        # non-causal calls without a mask, and masked calls with the causal flag folded into the mask)
+        first, m_seed = _seed_tiles(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, attn_mask, qpos, wide)
+        parts = []
+        for c in range(chunks):
+            lo = c * k_tiles // chunks
+            m_init = None if first is None else np.where(lo > first, m_seed, F32(-np.inf)).astype(F32)
+            parts.append(_online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, *krange(c, chunks),
+                                         attn_mask, qpos, wide, m_init=m_init))
         mm = parts[0][1]
         for _, mc, _ in parts[1:]:
             mm = np.maximum(mm, mc)
@@ -353,13 +374,50 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
         o = np.where(rows[..., None], oo, o)
         m = np.where(rows, mm, m)
         l = np.where(rows, ll, l)
-    with np.errstate(divide="ignore"):
-        inv = np.where(l > 0, (F32(1.0 / 448.0) / l).astype(F32), F32(0.0)).astype(F32)   # no visible key: 0
-    out = ((o * inv[..., None]).astype(F32) * vs[:, hk][:, :, None, :].astype(F32)).astype(F32)
-    out = round_output(out, out_dtype)
+    out = epilogue(o, l)
+    if also_unsplit:
+        assert not return_stats
+        return out, unsplit
     if return_stats:
         return out, m, l
     return out
+
+
+def _seed_tiles(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, attn_mask, qpos, wide):
+    """Per row: the first 64-key kernel tile that any row of its 128-row block sees (int [B, H, Sq]; a block that
+    sees no key gets a tile past the last), and the walk's running max after that tile.  (None, None) for a causal
+    call without a mask, which the kernel never splits."""
+    B, H, Sq = cl.shape
+    n_tiles = (seq_kv + block_n - 1) // block_n
+    per = KERNEL_TILE // block_n
+    k_tiles = (seq_kv + KERNEL_TILE - 1) // KERNEL_TILE
+    if attn_mask is None:
+        if causal:
+            return None, None
+        first = np.zeros((B, H, Sq), dtype=np.int64)
+    else:
+        rows, seq_q = qpos
+        vis = attn_mask if attn_mask.dtype == bool else attn_mask != -np.inf        # [B, H, Sq, seq_kv]
+        if causal:
+            vis = vis & (np.arange(seq_kv)[None, :] <= rows[:, None] + (seq_kv - seq_q))
+        tile_vis = np.zeros((B, H, Sq, k_tiles), dtype=bool)
+        for t in range(k_tiles):
+            tile_vis[..., t] = vis[..., t * KERNEL_TILE:(t + 1) * KERNEL_TILE].any(axis=-1)
+        blk = np.asarray(rows) // 128
+        first = np.full((B, H, Sq), k_tiles, dtype=np.int64)
+        for bb in np.unique(blk):
+            sel = blk == bb
+            any_t = tile_vis[:, :, sel].any(axis=2)                                   # [B, H, k_tiles]
+            f = np.where(any_t.any(-1), any_t.argmax(-1), k_tiles)
+            first[:, :, sel] = f[..., None]
+    m_seed = np.full((B, H, Sq), -np.inf, dtype=F32)
+    for f in np.unique(first):
+        if f >= k_tiles:
+            continue
+        m_f = _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, 0, min((f + 1) * per, n_tiles),
+                              attn_mask, qpos, wide)[1]
+        m_seed = np.where(first == f, m_f, m_seed).astype(F32)
+    return first, m_seed
 
 
 def wide_rows(cl, ks, seq_kv, pos, hk):
@@ -378,7 +436,7 @@ def wide_rows(cl, ks, seq_kv, pos, hk):
 
 
 def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo, t_hi, attn_mask=None,
-                    qpos=None, wide=None):
+                    qpos=None, wide=None, m_init=None):
     """Online softmax over key tiles [t_lo, t_hi): unnormalised O, running max m and sum l per row.  attn_mask:
     None, bool [B, H, Sq, seq_kv] (True = attend) or float32 [B, H, Sq, seq_kv] (additive, -inf = masked).  qpos:
     (the rows' positions in the query sequence, its length), default all Sq rows.
@@ -393,7 +451,7 @@ def _online_softmax(q8, cl, k8, ks, v8, seq_kv, causal, block_n, threshold, t_lo
     q8f = q8.astype(F32)
     k8f = k8.astype(F32)
     v8f = e4m3_to_f32(v8)
-    m = np.full((B, H, Sq), -np.inf, dtype=F32)
+    m = np.full((B, H, Sq), -np.inf, dtype=F32) if m_init is None else np.array(m_init, dtype=F32)
     l = np.zeros((B, H, Sq), dtype=F32)
     o = np.zeros((B, H, Sq, D), dtype=F32)
     rows, seq_q = qpos if qpos is not None else (np.arange(Sq), Sq)   # query positions, query length

@@ -12,6 +12,11 @@ N(mean, variance): N(0, 3) has standard deviation sqrt(3).
                                                                                   (HunyuanVideo)
   5a Q [2, 32, 8192, 128], K/V [2, 8, 8192, 128] bf16, N(0, 1), causal, return_lse  (GQA 4)
   5b Q [2, 16, 8192, 64],  K/V [2, 4, 8192, 64]  bf16, N(0, 1), causal, return_lse
+
+Two more shapes of the reference's model benchmark (tests/bench_models.py:27, :38; README.md:192, :196), for the head
+dims the configurations above do not time:
+  lumina    HND [1, 24, 4352, 96] bf16, N(0, 1)              (Neta Lumina 1024: head dim 96, no rotation)
+  auraflow  HND [2, 12, 4360, 256] fp16, N(0, 1)             (AuraFlow 1024 joint: head dim 256, batch 2)
 """
 from __future__ import annotations
 
@@ -66,6 +71,8 @@ CONFIGS = {
     "4": Config("hunyuan 1x24x67320x128", 4, 1, 24, 24, 67320, 128),
     "5a": Config("causal-gqa 2x32/8x8192x128", 5, 2, 32, 8, 8192, 128, causal=True, return_lse=True),
     "5b": Config("causal-gqa 2x16/4x8192x64", 5, 2, 16, 4, 8192, 64, causal=True, return_lse=True),
+    "lumina": Config("lumina 1x24x4352x96", 6, 1, 24, 24, 4352, 96),
+    "auraflow": Config("auraflow 2x12x4360x256", 7, 2, 12, 12, 4360, 256, dtype=torch.float16),
 }
 
 
@@ -78,7 +85,7 @@ def make_inputs(cfg: Config, heads: slice | None = None):
     heads that read them) after drawing the full tensors, so a sample matches the full problem bit for bit."""
     g = torch.Generator().manual_seed(cfg.seed)
     key = cfg.name.split()[0]
-    if key in ("plumbing", "causal-gqa"):
+    if key in ("plumbing", "causal-gqa", "lumina", "auraflow"):
         q, k, v = (_normal(g, s) for s in (cfg.shape_q, cfg.shape_kv, cfg.shape_kv))
     elif key == "flux":
         q, k, v = (_normal(g, s) for s in (cfg.shape_q, cfg.shape_kv, cfg.shape_kv))

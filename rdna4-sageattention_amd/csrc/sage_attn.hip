@@ -22,6 +22,9 @@
 // Passes.  Once every row of a wave has a max, a tile first runs without the block maxima: p with the current m,
 // kept when every lane's sum of 16 probabilities of each block stays below 2^7.5 (then no row's max can move), else
 // redone exactly (the maxima, the lazy-rescale decisions above, and a second pass when block 1 rescales).
+// Split tiles (the short last round of a launch): contiguous key ranges in parallel, merged by attn_merge_kernel; a
+// range after the block's first visited key tile starts from the max the one walk over every key has after that
+// tile (not from -inf), so it forms the walk's own probabilities wherever that max stays put.
 //
 // gfx950 mapping.  A workgroup owns 128 query rows (4 waves x 32) of one (batch, head) and walks the KV sequence
 // in 64-key tiles staged in LDS by direct global -> LDS loads (three buffers at head dims up to 128, the loads of the
@@ -234,7 +237,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   const float* ksq = ks + ((int64_t)khead * Skp + kofs) / SAGE_KV_BLOCK;
   const int nkb = (Skv + SAGE_KV_BLOCK - 1) / SAGE_KV_BLOCK;
   float kq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (SEEDED) {
+  // a packed sequence without keys (nkb = 0) reads no scale: its tile loop is empty and `wide` stays false
+  if (SEEDED && nkb > 0) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) kq[u] = ksq[min(64 * u + lane, nkb - 1)];
   }
@@ -280,6 +284,7 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   const uint8_t* bbase = nullptr;  // the same for the bias values of an additive mask (64 bytes per word)
   uint32_t boff = 0;
   const int* mcls = nullptr;
+  int mseed_tile = -1;  // MASK: the tile whose full pass seeds a split range's running max (-1: none)
   if (MASK) {
     const int64_t wslice = (int64_t)b * mt.bsb + (int64_t)h * mt.bsh;
     mbase = reinterpret_cast<const uint8_t*>(mbits_tab + wslice);
@@ -288,6 +293,8 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
     boff = (uint32_t)(((int64_t)qr * mt.bsq + hf) * 64);
     mcls = mcls_tab + (int64_t)b * mt.csb + (int64_t)h * mt.csh + (int64_t)min(q0 >> 5, mt.groups - 1) * mt.csg;
     const int2 r = mrange_tab[(int64_t)b * mt.rsb + (int64_t)h * mt.rsh + min(qt, mt.rblocks - 1)];
+    // a split range after the block's first visited tile starts from the walk's max after that tile (below)
+    if (split && t_lo > r.x && r.x < r.y) mseed_tile = r.x;
     t_lo = max(t_lo, r.x);
     t_hi = min(t_hi, r.y);
   }
@@ -604,14 +611,110 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   v16i seed16;
 #pragma unroll
   for (int v = 0; v < 16; ++v) seed16[v] = (int)SEED_BITS;
+  // A split key range after the first starts from the running max that one online softmax over every key has after
+  // the sequence's first tile (block 0 sets it, block 1 moves it by the lazy rule), instead of from -inf: the
+  // reference's max almost never moves after its first tile, so the range then forms the same probabilities, E4M3
+  // bytes and rescale decisions as the reference's walk (make_sage_r2.py:141-253) and its merge weight is l alone.
+  // The first tile's K goes into the buffer the loop fills last (free until the loop's first prefetch), beside the
+  // range's first tile(s); the dense split tiles are non-causal and unmasked and have at least 4 full key tiles.
+  const bool seed_split = !MASK && !VARLEN && split && t_lo > 0;
+  constexpr int SEED_BUF_OFS = NBUF - 1;  // buffer (t_lo + NBUF - 1) % NBUF
+  if (seed_split) {
+    const int8_t* kb_ = kbase;
+    asm volatile("" : "+s"(kb_));
+    uint8_t* dst_ = smem[(t_lo + SEED_BUF_OFS) % NBUF];
+#pragma unroll
+    for (int j = 0; j < KLOADS; ++j) {
+      asm volatile("" : "+v"(koff[j]));
+      copy16_to_lds(kb_ + koff[j], dst_ + (wave * KLOADS + j) * 1024);
+    }
+  }
+  if (MASK && mseed_tile >= 0) {
+    // The mask variant's seed: the block's first visited tile runs through the tile body of the wave's class (which
+    // sets m as the walk's first tile does, the mask and an additive bias included), then its l and O are dropped.
+    // It runs before the range's first tile is issued, which may reuse its buffer.
+    const int ts = mseed_tile;
+    SAGE_ISSUE_TILE(ts, ts % NBUF);
+    const int cs = mcls[ts];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (cs == 1) {
+      SAGE_TILE_PASSES(ts, 0, 0u, bw_none, wide);
+    } else if (cs == 2) {
+      const uint32_t mw = load_global_u32(mbase + (moff + 8u * (uint32_t)ts));
+      SAGE_TILE_PASSES(ts, 2, mw, bw_none, wide);
+    } else if (cs == 3) {
+      v4i bias_w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bias_w[i] = load_global_v4i(bbase + (boff + 128u * (uint32_t)ts + 16u * i));
+      SAGE_TILE_PASSES(ts, 3, 0u, bias_w, wide);
+    }
+    l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPV; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
+    __syncthreads();
+  }
   // the first tile (and, with three buffers, the second) in flight; wait for the first
   if (t_lo < t_hi) SAGE_ISSUE_TILE(t_lo, t_lo % NBUF);
-  if (NBUF == 3 && t_lo + 1 < t_hi) {
-    SAGE_ISSUE_TILE(t_lo + 1, (t_lo + 1) % NBUF);
-    wait_vmcnt<LPT>();
-  } else {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const bool two_ahead = NBUF == 3 && t_lo + 1 < t_hi;
+  if (two_ahead) SAGE_ISSUE_TILE(t_lo + 1, (t_lo + 1) % NBUF);
+  if (seed_split) {
+    // the first tile's K loads were issued before both tiles' loads
+    if constexpr (NBUF == 3) {
+      if (two_ahead)
+        wait_vmcnt<2 * LPT>();
+      else
+        wait_vmcnt<LPT>();
+    } else {
+      wait_vmcnt<LPT>();
+    }
+    tile_barrier();
+    const uint8_t* kt0 = smem[(t_lo + SEED_BUF_OFS) % NBUF];
+    v16i s0, s1;
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) {
+      const v4i k0_ = *reinterpret_cast<const v4i*>(kt0 + ko[i]);
+      const v4i k1_ = *reinterpret_cast<const v4i*>(kt0 + ko[i] + 32 * D);
+      s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0_, qa[i], i == 0 ? seed16 : s0, 0, 0, 0);
+      s1 = i == 0 ? mfma_i8_seeded<SEEDED>(k1_, qa[i]) : __builtin_amdgcn_mfma_i32_32x32x32_i8(k1_, qa[i], s1, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+    // the two 32-key blocks' maxima in m's units (as the exact pass takes them)
+    float mxh;
+    if (SEEDED) {
+      int mi0 = s0[0], mi1 = s1[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) {
+        mi0 = max(mi0, s0[v]);
+        mi1 = max(mi1, s1[v]);
+      }
+      mxh = __int_as_float(halves_max_i32(mi0, mi1));
+    } else {
+      float mx0 = (float)s0[0], mx1 = (float)s1[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) {
+        mx0 = fmaxf(mx0, (float)s0[v]);
+        mx1 = fmaxf(mx1, (float)s1[v]);
+      }
+      mxh = halves_max_f32(mx0, mx1);
+    }
+    const float ksh = hf ? ksb[1] : ksb[0];
+    const float bmh = SEEDED ? (mxh - SEED_F) * ksh : mxh * ksh;
+    float bm0, bm1;
+    halves_split_f32(bmh, bm0, bm1);
+    // from m = -inf block 0 always sets the max (its keys are all visible); block 1 moves it by the lazy rule
+    const float mc1 = fmaxf(bm0, bm1);
+    m = (mc1 - bm0) * cl > 8.0f ? mc1 : bm0;
+    negm = 0.0f - cl * m;
+    if (SPEC_OK) fastok = true;
   }
+  if (two_ahead)
+    wait_vmcnt<LPT>();
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   tile_barrier();
   int t = t_lo;
   if (MASK) {

@@ -13,7 +13,7 @@ import torch.nn.functional as F
 
 import cdna4_sage
 from cdna4_sage import _capi
-from gpu_util import cosine, hnd_np, kv_split
+from gpu_util import assert_near_walk, cosine, hnd_np, kv_split
 from oracle import sage_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -37,14 +37,17 @@ def _inputs(B, H, Hkv, Sq, Skv, D, dt, layout, seed=0):
 
 
 def _emulate(q, k, v, layout, causal, mask, split, out_dtype):
+    """Emulation with the mask following the kernel's split plan, float64 attention, and the reference's one walk
+    over every key (None when the plan splits nothing)."""
     qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
     q8, qs = orc.quant_q(qn)
     k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(kn.shape[2]))
     m = mask.cpu().numpy() if mask.dtype == torch.bool else mask.float().cpu().numpy()
     emu = orc.attention(q8, qs, k8, ks, v8, vs, kn.shape[2], causal=causal, block_n=32, out_dtype=out_dtype,
-                        kv_split=split, attn_mask=m)
+                        kv_split=split, attn_mask=m, also_unsplit=split is not None)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, attn_mask=m)
-    return emu, ref
+    emu, walk = emu if split is not None else (emu, None)
+    return emu, ref, walk
 
 
 def _key_padding(B, Skv, lengths):
@@ -105,12 +108,14 @@ def test_masked_attention_vs_emulation(dev, name, shape, make_mask):
     assert np.isfinite(got).all()
     split = kv_split(dev, B, H, Sq, Skv, D, False)   # the masked call uses the dense non-causal plan
     full = torch.broadcast_to(mask, (B, H, Sq, Skv))
-    emu, ref = _emulate(q, k, v, layout, causal, full, split, "bf16" if dt == torch.bfloat16 else "f16")
+    emu, ref, walk = _emulate(q, k, v, layout, causal, full, split, "bf16" if dt == torch.bfloat16 else "f16")
     err = float(np.abs(got - emu).max())
     assert err <= MAX_ABS, err
     assert cosine(got, ref) >= COS
     assert float((got == emu).mean()) >= SAME_BITS[dt]
     assert err <= MAX_REL * float(np.abs(emu).max())
+    if walk is not None:   # split tiles, also against the reference's one walk over every key
+        assert_near_walk(got, walk, ref)
     if name == "random full":
         assert (got[0, 1, 7] == 0).all() and (ref[0, 1, 7] == 0).all()
         assert np.abs(got[0, 0, 9] - emu[0, 0, 9]).max() <= MAX_ABS
@@ -222,12 +227,14 @@ def test_float_mask_vs_emulation(dev, name, shape, make_mask):
     assert np.isfinite(got).all()
     split = kv_split(dev, B, H, Sq, Skv, D, False)
     full = torch.broadcast_to(mask, (B, H, Sq, Skv))
-    emu, ref = _emulate(q, k, v, layout, causal, full, split, "bf16" if dt == torch.bfloat16 else "f16")
+    emu, ref, walk = _emulate(q, k, v, layout, causal, full, split, "bf16" if dt == torch.bfloat16 else "f16")
     err = float(np.abs(got - emu).max())
     assert err <= MAX_ABS, err
     assert cosine(got, ref) >= COS
     assert float((got == emu).mean()) >= SAME_BITS[dt]
     assert err <= MAX_REL * float(np.abs(emu).max())
+    if walk is not None:   # split tiles, also against the reference's one walk over every key
+        assert_near_walk(got, walk, ref)
 
 
 def test_float_mask_identities(dev):

@@ -13,7 +13,7 @@ import torch
 
 import cdna4_sage
 from cdna4_sage import _capi
-from gpu_util import cosine, hnd_np, kv_split
+from gpu_util import assert_near_walk, cosine, hnd_np, kv_split
 from oracle import sage_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -77,14 +77,18 @@ def test_random_shapes_vs_emulation(dev, case):
     qn, kn, vn = hnd_np(q, layout), hnd_np(k, layout), hnd_np(v, layout)
     q8, qs = orc.quant_q(qn, sm)
     k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(Skv))
+    split = kv_split(dev, B, H, Sq, Skv, D, causal)
     emu = orc.attention(q8, qs, k8, ks, v8, vs, Skv, causal=causal, block_n=32,
-                        out_dtype="bf16" if dt == torch.bfloat16 else "f16",
-                        kv_split=kv_split(dev, B, H, Sq, Skv, D, causal))
+                        out_dtype="bf16" if dt == torch.bfloat16 else "f16", kv_split=split,
+                        also_unsplit=split is not None)
+    emu, walk = emu if split is not None else (emu, None)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, sm_scale=sm)
     err = float(np.abs(got - emu).max())
     assert err <= max(MAX_ABS, REL * float(np.abs(emu).max())), (err, float(np.abs(emu).max()))
     assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
     assert float((got == emu).mean()) >= SAME_BITS[dt]
+    if walk is not None:   # split tiles, also against the reference's one walk over every key
+        assert_near_walk(got, walk, ref)
 
 
 def _mask_cases(n=20, seed=777):
@@ -143,11 +147,15 @@ def test_random_masks_vs_emulation(dev, case):
     k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(Skv))
     m = torch.broadcast_to(mask, (B, H, Sq, Skv))
     m = m.numpy() if kind == "bool" else m.float().numpy()
+    split = kv_split(dev, B, H, Sq, Skv, D, False)
     emu = orc.attention(q8, qs, k8, ks, v8, vs, Skv, causal=causal, block_n=32,
-                        out_dtype="bf16" if dt == torch.bfloat16 else "f16",
-                        kv_split=kv_split(dev, B, H, Sq, Skv, D, False), attn_mask=m)
+                        out_dtype="bf16" if dt == torch.bfloat16 else "f16", kv_split=split, attn_mask=m,
+                        also_unsplit=split is not None)
+    emu, walk = emu if split is not None else (emu, None)
     ref = orc.sdpa_reference(qn, kn, vn, causal=causal, attn_mask=m)
     err = float(np.abs(got - emu).max())
     assert err <= max(MAX_ABS, REL * float(np.abs(emu).max())), (err, float(np.abs(emu).max()))
     assert cosine(got, ref) >= min(COS, cosine(emu, ref) - 1e-4)
     assert float((got == emu).mean()) >= SAME_BITS[dt]
+    if walk is not None:
+        assert_near_walk(got, walk, ref)

@@ -139,6 +139,8 @@ VARLEN_CASES = [  # lq, lk, H, Hkv, D, dtype, causal
     ([1000, 3, 1], [1000, 3, 1], 8, 8, 64, torch.bfloat16, False),
     ([300, 90, 700], [500, 90, 650], 4, 2, 96, torch.bfloat16, True),
     ([200, 333], [260, 700], 2, 1, 256, torch.float16, False),
+    ([100, 300], [0, 500], 4, 2, 128, torch.bfloat16, False),                    # sequence 0 (first rows) has no keys
+    ([70, 130, 200], [0, 0, 300], 2, 1, 64, torch.float16, True),
 ]
 
 

@@ -68,3 +68,36 @@ def test_noalloc_rejects_a_shape_beyond_its_array(dev):
         _capi.call("sage_forward_noalloc", q.data_ptr(), *_hnd(q), q.data_ptr(), *_hnd(q), q.data_ptr(), *_hnd(q),
                    q.data_ptr(), 0, 128, 128, 1, 40, 40, 32760, 32760, 128, 0, 0, 1.0,
                    torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _noalloc_call(q, k, v, out):
+    """sage_forward_noalloc on torch's current stream, no synchronisation (so that it can be captured)."""
+    B, H, S, D = q.shape
+    _capi.call("sage_forward_noalloc", q.data_ptr(), *_hnd(q), k.data_ptr(), *_hnd(k), v.data_ptr(), *_hnd(v),
+               out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), B, H, k.shape[1], S, S, D, DT[q.dtype], 0,
+               1.0, torch.cuda.current_stream(q.device).cuda_stream)
+
+
+def test_noalloc_replays_under_graph_capture(dev):
+    """After one eager call on the GPU (which looks up the array's address), a captured sage_forward_noalloc replays
+    bit-equal to sage_forward, also when an eager call with another, smaller problem ran on the same array between
+    the replays (the replay recomputes every intermediate)."""
+    B, H, Hkv, S, D = 1, 8, 4, 1500, 128
+    q, k, v = (t.to(dev) for t in _inputs(B, H, Hkv, S, D, torch.bfloat16, seed=41))
+    ref = _forward(q, k, v, False, noalloc=False)
+    out = torch.empty(B, S, H, D, dtype=q.dtype, device=dev)
+    _noalloc_call(q, k, v, out)                                     # eager, before the capture
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out, ref)
+    q2, k2, v2 = (t.to(dev) for t in _inputs(1, 4, 2, 700, 64, torch.float16, seed=42))
+    ref2 = _forward(q2, k2, v2, False, noalloc=False)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _noalloc_call(q, k, v, out)
+    for i in range(3):
+        out.fill_(3.0)
+        got2 = _forward(q2, k2, v2, False, noalloc=True)            # another problem on the same array, eager
+        assert torch.equal(got2, ref2), i
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out, ref), i
