@@ -147,6 +147,24 @@ MODEL_SHAPES = [
 ]
 
 
+def intermediates(cfg, dev):
+    """Q8, QS, K8, KS, V8T, VS of one sage_forward call on cfg, in the C ABI's layouts (include/sage_capi.h): the
+    int8 / E4M3 rows have sage_layout_dim(D) channels (128 for head dim 96, zero-padded), the key axis
+    sage_kv_pad(S) rows."""
+    import torch
+
+    from cdna4_sage import _capi
+
+    B, H, Hkv, S, D = cfg.B, cfg.H, cfg.Hkv, cfg.S, cfg.D
+    skp, dl = _capi.kv_pad(S), _capi.layout_dim(D)
+    return (torch.empty(B, H, S, dl, dtype=torch.int8, device=dev),
+            torch.empty(B, H, S, dtype=torch.float32, device=dev),
+            torch.empty(B, Hkv, skp, dl, dtype=torch.int8, device=dev),
+            torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev),
+            torch.empty(B, Hkv, dl, skp, dtype=torch.uint8, device=dev),
+            torch.empty(B, Hkv, dl, dtype=torch.float32, device=dev))
+
+
 def median_synced_ms(fn, n=10):
     """The reference's per-call time: 3 warm-up calls, then the median of n calls each followed by a sync."""
     import torch
@@ -281,12 +299,7 @@ def main():
     B, H, Hkv, S, D = cfg.B, cfg.H, cfg.Hkv, cfg.S, cfg.D
     skp = _capi.kv_pad(S)
     st = torch.cuda.current_stream(dev).cuda_stream
-    q8 = torch.empty(B, H, S, D, dtype=torch.int8, device=dev)
-    qs = torch.empty(B, H, S, dtype=torch.float32, device=dev)
-    k8 = torch.empty(B, Hkv, skp, D, dtype=torch.int8, device=dev)
-    ks = torch.empty(B, Hkv, skp // 32, dtype=torch.float32, device=dev)
-    v8t = torch.empty(B, Hkv, D, skp, dtype=torch.uint8, device=dev)
-    vs = torch.empty(B, Hkv, D, dtype=torch.float32, device=dev)
+    q8, qs, k8, ks, v8t, vs = intermediates(cfg, dev)
     out = torch.empty(B, S, H, D, dtype=q.dtype, device=dev)
     hs = (q.stride(0), q.stride(2), q.stride(1))
     ks_ = (k.stride(0), k.stride(2), k.stride(1))

@@ -229,3 +229,21 @@ def test_forward_noalloc_rejects_before_touching_the_gpu():
     assert rc == _capi.SAGE_ERR_INVALID and "scratch" in _err() and str(128 << 20) in _err()
     # the array's own size: 128 MiB, the value the header states
     assert "(128ll << 20)" in HEADER.read_text()
+
+
+def test_bench_intermediates_have_the_abi_layout_sizes():
+    """bench.py hands its own Q8 / QS / K8 / KS / V8T / VS to sage_forward and sage_attn_fwd, which cannot check
+    buffer sizes: every configuration's buffers must have the sizes of include/sage_capi.h's layouts (int8 / E4M3
+    rows of 128 channels for head dim 96, keys padded to 128).  Head-dim-sized buffers for the d96 configuration were
+    written past their end on the GPU."""
+    import bench
+    from cdna4_sage.configs import CONFIGS
+
+    for name, cfg in CONFIGS.items():
+        B, H, Hkv, S, D = cfg.B, cfg.H, cfg.Hkv, cfg.S, cfg.D
+        dl = 128 if D == 96 else D
+        skp = (S + 127) // 128 * 128
+        want = [B * H * S * dl, 4 * B * H * S, B * Hkv * skp * dl, 4 * B * Hkv * skp // 32, B * Hkv * dl * skp,
+                4 * B * Hkv * dl]
+        got = [t.numel() * t.element_size() for t in bench.intermediates(cfg, "meta")]
+        assert got == want, (name, got, want)
