@@ -46,6 +46,9 @@ MIN_KV = _env_int(("CDNA4_SAGE_MIN_KV", "RDNA4_SAGE_MIN_KV"), 1024)
 # attn_masks (bool, or additive of q's dtype) run on the kernel (quantized like every other call); 0 restores the
 # reference's SDPA routing.
 NATIVE_MASK = _env_int(("CDNA4_SAGE_NATIVE_MASK",), 1) != 0
+# sageattention.sageattn_varlen routes every sequence of a packed batch as the reference does (offsets read back, the
+# short sequences to SDPA); 0 runs one quantized pass over every sequence without reading the offsets back.
+VARLEN_ROUTE = _env_int(("CDNA4_SAGE_VARLEN_ROUTE",), 1) != 0
 
 
 def is_available(device=None) -> bool:

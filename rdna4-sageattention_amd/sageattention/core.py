@@ -121,33 +121,62 @@ def sageattn_varlen(
     **kwargs: Any,
 ) -> torch.Tensor:
     """Sequences packed along the token axis: q is [sum of query lengths, heads, head_dim], k and v
-    [sum of key lengths, kv heads, head_dim]; cu_seqlens_q / cu_seqlens_k hold the batch + 1 sequence offsets
-    (reference: src/sageattention/core.py:66-89, which loops over the sequences on the host after reading the
-    offsets back).
-    On gfx950, when the longest key sequence reaches the kernel's minimum length (max_seqlen_k >= MIN_KV, or unknown),
-    the whole batch runs in one stream-ordered pass of the int8/fp8 kernels with per-sequence scales and no host
-    synchronisation; sequences that a per-sequence call would send to SDPA for being short are quantized there too.
-    Otherwise each sequence is routed like a sageattn call; empty query sequences are skipped."""
+    [sum of key lengths, kv heads, head_dim]; cu_seqlens_q / cu_seqlens_k hold the batch + 1 sequence offsets.
+
+    The reference reads the offsets back to the host and sends every sequence through sageattn on its own
+    (src/sageattention/core.py:80-88), so each sequence takes sageattn's route: the quantized kernel when it is long
+    enough (kv_len >= MIN_KV and heads * q_len * kv_len, halved when causal, >= MIN_WORK), torch SDPA otherwise.  This
+    does the same: after reading the offsets, the sequences the kernel takes run in one packed stream-ordered pass of
+    the int8/fp8 kernels (bit-equal, per sequence, to a call on that sequence with every query tile whole), and the
+    others through sageattn one by one.  Under graph capture or torch.compile tracing, where the offsets cannot be
+    read back, or with CDNA4_SAGE_VARLEN_ROUTE=0, the packed pass takes every sequence (no host synchronisation; the
+    short ones are then quantized too).  Without a gfx950 GPU, or when the longest key sequence is below MIN_KV, every
+    sequence goes through sageattn; empty query sequences are skipped."""
     try:
         mk = None if max_seqlen_k is None else int(max_seqlen_k)
     except (TypeError, ValueError):
         mk = None
     if q.is_cuda and (mk is None or mk >= cdna4_sage.MIN_KV):
+        sync_free = (not cdna4_sage.VARLEN_ROUTE or torch.compiler.is_compiling()
+                     or torch.cuda.is_current_stream_capturing())
         try:
-            return cdna4_sage.attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                                               sm_scale=sm_scale, is_causal=is_causal)
+            if sync_free:
+                return cdna4_sage.attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                                   sm_scale=sm_scale, is_causal=is_causal)
+            seqs = _sequences(cu_seqlens_q, cu_seqlens_k)
+            fast = [_kernel_takes(q1 - q0, k1 - k0, q.shape[1], is_causal) for q0, q1, k0, k1 in seqs]
+            if any(fast):
+                out = cdna4_sage.attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                                  sm_scale=sm_scale, is_causal=is_causal)
+                for (q0, q1, k0, k1), f in zip(seqs, fast):
+                    if not f:
+                        out[q0:q1] = _one_sequence(q, k, v, q0, q1, k0, k1, is_causal, sm_scale)
+                return out
         except cdna4_sage.Unsupported:
             pass
+    out = torch.empty_like(q)
+    for q0, q1, k0, k1 in _sequences(cu_seqlens_q, cu_seqlens_k):
+        out[q0:q1] = _one_sequence(q, k, v, q0, q1, k0, k1, is_causal, sm_scale)
+    return out
+
+
+def _sequences(cu_seqlens_q, cu_seqlens_k):
+    """(q0, q1, k0, k1) of every sequence with at least one query, from offsets read back to the host."""
     bq = [int(x) for x in cu_seqlens_q.tolist()]
     bk = [int(x) for x in cu_seqlens_k.tolist()]
-    out = torch.empty_like(q)
-    for (q0, q1), (k0, k1) in zip(zip(bq[:-1], bq[1:]), zip(bk[:-1], bk[1:])):
-        if q1 == q0:
-            continue
-        o = sageattn(q[q0:q1].unsqueeze(0), k[k0:k1].unsqueeze(0), v[k0:k1].unsqueeze(0), tensor_layout="NHD",
-                     is_causal=is_causal, sm_scale=sm_scale)
-        out[q0:q1] = o[0]
-    return out
+    return [(q0, q1, k0, k1) for (q0, q1), (k0, k1) in zip(zip(bq[:-1], bq[1:]), zip(bk[:-1], bk[1:])) if q1 > q0]
+
+
+def _kernel_takes(sq, skv, heads, is_causal):
+    """Whether sageattn on one sequence of a packed batch runs the kernel: the router's size rule (cdna4_sage._worth_it
+    with batch 1) and the kernel's causal shapes (q_len <= kv_len)."""
+    work = heads * sq * skv // (2 if is_causal else 1)
+    return skv >= cdna4_sage.MIN_KV and work >= cdna4_sage.MIN_WORK and not (is_causal and sq > skv)
+
+
+def _one_sequence(q, k, v, q0, q1, k0, k1, is_causal, sm_scale):
+    return sageattn(q[q0:q1].unsqueeze(0), k[k0:k1].unsqueeze(0), v[k0:k1].unsqueeze(0), tensor_layout="NHD",
+                    is_causal=is_causal, sm_scale=sm_scale)[0]
 
 
 def _variant(q, k, v, tensor_layout="HND", is_causal=False, sm_scale=None, return_lse=False, **kwargs):

@@ -176,8 +176,22 @@ def test_varlen_python_api_and_router(dev):
     out = cdna4_sage.attention_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), is_causal=True)
     r = _varlen_capi(qd, kd, vd, cu_q, cu_k, True)
     assert torch.equal(out[:4300], r["out"][:4300])
+    # the reference's route for each sequence: with 8 heads none of these reaches MIN_WORK (1500^2 * 8 / 2 < 64 Mi), so
+    # sageattn_varlen gives what one sageattn call per sequence gives (SDPA here), as the reference's host loop does
     routed = sageattention.sageattn_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), is_causal=True)
-    assert torch.equal(routed, out)
+    for (q0, q1), (k0, k1) in zip(zip(cu_q[:-1], cu_q[1:]), zip(cu_k[:-1], cu_k[1:])):
+        if q1 > q0:
+            one = sageattention.sageattn(qd[q0:q1].unsqueeze(0), kd[k0:k1].unsqueeze(0), vd[k0:k1].unsqueeze(0),
+                                         tensor_layout="NHD", is_causal=True)[0]
+            assert torch.equal(routed[q0:q1], one)
+    # without the per-sequence route (CDNA4_SAGE_VARLEN_ROUTE=0) every sequence runs the packed pass, unsynchronised
+    import cdna4_sage as cs
+    saved = cs.VARLEN_ROUTE
+    try:
+        cs.VARLEN_ROUTE = False
+        assert torch.equal(sageattention.sageattn_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), is_causal=True), out)
+    finally:
+        cs.VARLEN_ROUTE = saved
     # sm_scale folds into the Q scales as in the dense path: sequence 0 against float32 attention at that scale
     o2 = cdna4_sage.attention_varlen(qd, kd, vd, cq, ck, sm_scale=0.05)
     q0 = qd[:1500].transpose(0, 1).float().contiguous()                               # [8, 1500, 128]
@@ -199,6 +213,38 @@ def test_varlen_python_api_and_router(dev):
         ref = torch.nn.functional.scaled_dot_product_attention(
             qd[q0:q1].transpose(0, 1).float(), kd[k0:k1].transpose(0, 1).float(), vd[k0:k1].transpose(0, 1).float())
         torch.testing.assert_close(small[q0:q1].float(), ref.transpose(0, 1), atol=2e-2, rtol=0)
+
+
+def test_varlen_routes_each_sequence_like_the_reference(dev):
+    """A batch whose sequences take both routes of the reference's per-sequence sageattn calls
+    (src/sageattention/core.py:80-88): sequences 0 and 2 reach MIN_KV and MIN_WORK with 8 heads and run the packed
+    kernel pass (bit-equal to the pass on the whole batch), sequence 1 (500 keys) and the causal sequence longer than
+    its keys go to sageattn alone (torch SDPA, exact), an empty query sequence is skipped."""
+    for causal, lq, lk in ((False, [3000, 500, 0, 2900], [3000, 500, 40, 2900]),
+                           (True, [4200, 900, 4300], [4200, 600, 4300])):
+        q, k, v, cu_q, cu_k = _packed(lq, lk, 8, 4, 128, torch.bfloat16, seed=31 + causal)
+        qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+        cq, ck = torch.tensor(cu_q, device=dev), torch.tensor(cu_k, device=dev)
+        routed = sageattention.sageattn_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), is_causal=causal)
+        packed = cdna4_sage.attention_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), is_causal=causal)
+        kinds = []
+        for (q0, q1), (k0, k1) in zip(zip(cu_q[:-1], cu_q[1:]), zip(cu_k[:-1], cu_k[1:])):
+            if q1 == q0:
+                continue
+            work = 8 * (q1 - q0) * (k1 - k0) // (2 if causal else 1)
+            kernel = (k1 - k0) >= cdna4_sage.MIN_KV and work >= cdna4_sage.MIN_WORK and not (causal and q1 - q0 > k1 - k0)
+            kinds.append(kernel)
+            if kernel:
+                assert torch.equal(routed[q0:q1], packed[q0:q1])
+            else:
+                ref = torch.nn.functional.scaled_dot_product_attention(
+                    qd[q0:q1].transpose(0, 1)[None], kd[k0:k1].transpose(0, 1)[None], vd[k0:k1].transpose(0, 1)[None],
+                    is_causal=False, enable_gqa=True,
+                    attn_mask=(torch.ones(q1 - q0, k1 - k0, dtype=torch.bool, device=dev).tril(int(k1 - k0) - int(q1 - q0))
+                               if causal else None))
+                torch.testing.assert_close(routed[q0:q1].float(), ref[0].transpose(0, 1).float(), atol=1e-2, rtol=0)
+                assert not torch.equal(routed[q0:q1], packed[q0:q1])
+        assert any(kinds) and not all(kinds), kinds
 
 
 def test_varlen_mixed_lengths_at_scale(dev):
