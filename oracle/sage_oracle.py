@@ -364,9 +364,12 @@ def attention(q8, qs, k8, ks, v8, vs, seq_kv: int, causal: bool = False, block_n
         for oc, mc, lc in parts:
             # each chunk's O is stored normalised by its own l, in fp16 (round to nearest even); a chunk without
             # a visible key (l = 0) stores 0 and weighs 0
-            with np.errstate(divide="ignore", invalid="ignore"):
-                rl = np.where(lc > 0, (F32(1.0) / lc).astype(F32), F32(0.0)).astype(F32)
-                pn = (oc * rl[..., None]).astype(F32).astype(np.float16).astype(F32)
+            # (below 2^-64, l and O are scaled by 2^64 first, exactly, so that the reciprocal stays finite: a range
+            # started from the seeded max can hold only probabilities far below it)
+            with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+                ls = np.where(lc < F32(2.0 ** -64), F32(2.0 ** 64), F32(1.0)).astype(F32)
+                rl = np.where(lc > 0, (F32(1.0) / (lc * ls).astype(F32)).astype(F32), F32(0.0)).astype(F32)
+                pn = ((oc * ls[..., None]).astype(F32) * rl[..., None]).astype(F32).astype(np.float16).astype(F32)
                 w = np.where(lc > 0, (np.exp2(((mc - mm).astype(F32) * cl).astype(F32)).astype(F32) * lc).astype(F32),
                              F32(0.0)).astype(F32)
             ll = (ll + w).astype(F32)

@@ -812,14 +812,18 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
   if (split) {
     // partial state of this key range (workspace layout at ws_ml_offset), merged by attn_merge_kernel
     const int q = wave * 32 + ln;
-    const float rl = lt > 0.0f ? 1.0f / lt : 0.0f;  // a range in which the row sees no key stores 0
+    // A range that starts from the seeded max may hold only probabilities far below it, so l can be tiny (down to
+    // subnormal, with every E4M3 byte 0 and O = 0): below 2^-64 both l and O are scaled by 2^64 (exact) before the
+    // reciprocal, which then stays finite; l and O of order 1 and above are used as they are.
+    const float ls = lt < 0x1p-64f ? 0x1p64f : 1.0f;
+    const float rl = lt > 0.0f ? 1.0f / (lt * ls) : 0.0f;  // a range in which the row sees no key stores 0
     uint16_t* po = reinterpret_cast<uint16_t*>(part) + ((int64_t)unit * ATT_BM + q) * D;
 #pragma unroll
     for (int i = 0; i < NPV; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const uint32_t h0 = f32_to_f16_bits(o[i][4 * g + 0] * rl), h1 = f32_to_f16_bits(o[i][4 * g + 1] * rl);
-        const uint32_t h2 = f32_to_f16_bits(o[i][4 * g + 2] * rl), h3 = f32_to_f16_bits(o[i][4 * g + 3] * rl);
+        const uint32_t h0 = f32_to_f16_bits((o[i][4 * g + 0] * ls) * rl), h1 = f32_to_f16_bits((o[i][4 * g + 1] * ls) * rl);
+        const uint32_t h2 = f32_to_f16_bits((o[i][4 * g + 2] * ls) * rl), h3 = f32_to_f16_bits((o[i][4 * g + 3] * ls) * rl);
         *reinterpret_cast<uint2*>(po + 32 * i + 8 * g + 4 * hf) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
       }
     const int64_t units = (int64_t)(total - n_full) * chunks;

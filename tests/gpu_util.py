@@ -98,3 +98,20 @@ def assert_near_walk(got, walk, ref):
     own = float(np.abs(np.asarray(walk, np.float64) - ref).max())
     assert gap <= max(WALK_MAX_ABS, own), (gap, own)
     return gap
+
+
+def underflow_split_inputs(seed=3):
+    """One head (Sq 128, Skv 1024, head dim 128, bf16 values as float32 [1, 1, S, 128]) whose query rows all point
+    along one direction u: key 0 is 20 u, every other key -16 u (plus noise), the rows 30 u times 0.9 to 1.1.  Key 0
+    leads every other key by ~124 to ~152 in the exponent (log2 units), so a split range that starts from the
+    running max after key tile 0 holds only probabilities of 2^-124 to 2^-152: its l falls below 2^-128, or to 0,
+    and every E4M3 byte of its P is 0.  The output is V of key 0."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(128, generator=g)
+    u = u / u.norm()
+    f = 0.9 + 0.2 * torch.rand(128, 1, generator=g)
+    q = 30.0 * f * u + 0.02 * torch.randn(128, 128, generator=g)
+    k = -16.0 * u + 0.02 * torch.randn(1024, 128, generator=g)
+    k[0] = 20.0 * u
+    v = torch.randn(1024, 128, generator=g)
+    return [t[None, None].to(torch.bfloat16).float().numpy() for t in (q, k, v)]

@@ -168,6 +168,26 @@ def test_split_plan_and_unsplit_call(dev, B, H, Sq, Skv, D):
     assert_near_walk(outs[1], whole, ref)   # the split call against the reference's one walk over every key
 
 
+def test_split_range_whose_probabilities_underflow(dev):
+    """Key 0 leads every other key by 124-152 in the exponent: the later ranges of the split (plan: one tile, 4
+    ranges), started from the max after key tile 0, hold l in (0, 2^-128) on most rows and O = 0.  The kernel must
+    store their partials as 0 (no 0 * inf = NaN from 1 / l) and give the emulation's output, V of key 0."""
+    from gpu_util import underflow_split_inputs
+
+    q, k, v = underflow_split_inputs()
+    split = kv_split(dev, 1, 1, 128, 1024, 128, False)
+    assert split is not None and split[0] >= 2
+    qt, kt, vt = (torch.from_numpy(a).to(torch.bfloat16) for a in (q, k, v))
+    out = cdna4_sage.attention(qt.to(dev), kt.to(dev), vt.to(dev), "HND")
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v, seq_pad=_capi.kv_pad(1024))
+    emu, walk = orc.attention(q8, qs, k8, ks, v8, vs, 1024, block_n=32, kv_split=split, also_unsplit=True)
+    assert float(np.abs(got - emu).max()) <= MAX_ABS
+    assert_near_walk(got, walk, orc.sdpa_reference(q, k, v))
+
+
 def test_split_merge_is_deterministic_across_calls(dev):
     """Split tiles are merged from partials in a workspace that every call reuses.  Repeated calls that alternate
     two inputs must reproduce each output bit for bit: a merge that read stale partials of the previous call, or

@@ -483,6 +483,32 @@ def test_split_ranges_stay_near_the_reference_walk(kind, chunks, max_gap):
         assert float(np.abs(_split_from_minus_inf(q8, cl, k8, ks, v8, vs, skv, chunks, rows) - walk).max()) > max_gap
 
 
+def test_split_range_whose_probabilities_underflow_against_the_seed():
+    """A range that starts from the seeded max can hold only probabilities far below it: with key 0 leading every
+    other key by 124-152 in the exponent, each later range of the 4-range split has l in (0, 2^-128) on 72 of the 128
+    rows (l = 0 on 14) and O = 0 (every E4M3 byte of P is 0).  1 / l overflows there; the stored partial must still
+    be 0 (l and O scaled by 2^64 before the reciprocal), not 0 * inf = NaN, and the merge must give the walk's output
+    (V of key 0) up to the fp16 rounding of the first range's O / l (one bf16 step of outputs up to ~4)."""
+    from gpu_util import underflow_split_inputs
+
+    q, k, v = underflow_split_inputs()
+    q8, qs = orc.quant_q(q)
+    k8, ks, v8, vs = orc.quant_kv(k, v, seq_pad=1024)
+    out, walk = orc.attention(q8, qs, k8, ks, v8, vs, 1024, block_n=32, kv_split=(4, np.ones((1, 1, 128), bool)),
+                              also_unsplit=True)
+    assert np.isfinite(out).all()
+    assert float(np.abs(out - walk).max()) <= 2.0 ** -6
+    assert float(np.abs(walk - orc.sdpa_reference(q, k, v)).max()) <= 0.1
+    # the case does reach the overflow: some range has 0 < l < 2^-128 after the seeded start
+    cl = (orc.logit_scale_base(128) * qs).astype(F32)
+    rows = (np.arange(128), 128)
+    wide = orc.wide_rows(cl, ks, 1024, rows[0], np.arange(1))
+    _, m_seed = orc._seed_tiles(q8, cl, k8, ks, v8, 1024, False, 32, orc.RESCALE_THRESHOLD, None, rows, wide)
+    o, _, l = orc._online_softmax(q8, cl, k8, ks, v8, 1024, False, 32, orc.RESCALE_THRESHOLD, 8, 16, None, rows, wide,
+                                  m_init=m_seed)
+    assert int(((l > 0) & (l < F32(2.0 ** -128))).sum()) > 0 and not o.any()
+
+
 def _split_from_minus_inf(q8, cl, k8, ks, v8, vs, seq_kv, chunks, rows):
     """The merged split with every range's softmax from m = -inf (the previous kernel's split; bf16 output)."""
     qpos = (rows, seq_kv)
