@@ -832,17 +832,24 @@ __global__ __launch_bounds__(ATT_THREADS, attn_occupancy<layout_dim(HD)>()) void
           make_float2(m * SSCALE, lt);  // m in S * ks units, as the merge kernel's cl expects
     return;
   }
+  // The lane's V scales (its 4 * NPV groups of 4 channels), every load issued before the first is used: one round
+  // trip instead of one per channel block.  VS rows hold D channels, so the loads stay in bounds for head_dim 96 too.
+  const float* vsr = vs + (int64_t)bhk * D;
+  v4f sc[NPV][4];
+#pragma unroll
+  for (int i = 0; i < NPV; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sc[i][g] = *reinterpret_cast<const v4f*>(vsr + 32 * i + 8 * g + 4 * hf);
   const float inv = lt > 0.0f ? (1.0f / 448.0f) / lt : 0.0f;  // a row without any visible key is written as 0
   if (qvalid) {
     uint16_t* orow = obase + (int64_t)qrow * oss + h * osh;
-    const float* vsr = vs + (int64_t)bhk * D;
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
       if (32 * i >= dout) break;  // head_dim 96: the zero-padded channels are not written
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c = 32 * i + 8 * g + 4 * hf;
-        const v4f sc4 = *reinterpret_cast<const v4f*>(vsr + c);
+        const v4f sc4 = sc[i][g];
         const uint32_t e0 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 0] * inv) * sc4[0]);
         const uint32_t e1 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 1] * inv) * sc4[1]);
         const uint32_t e2 = f32_to_out_bits<OUT_DT>((o[i][4 * g + 2] * inv) * sc4[2]);
@@ -886,6 +893,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   const float2* ml =
       reinterpret_cast<const float2*>(reinterpret_cast<const uint8_t*>(part) + ws_ml_offset(units, D)) + unit0 * ATT_BM + q;
   const uint16_t* po = reinterpret_cast<const uint16_t*>(part) + (unit0 * ATT_BM + q) * D + 4 * cg;
+  // the row's Q scale and the group's V scales first, so that every load of the thread is in flight at once (loaded
+  // after the merge arithmetic, the V scales cost a second round trip)
+  const float qsr = qs[(int64_t)bh * Sq + qrow];
+  const v4f sc4 = *reinterpret_cast<const v4f*>(vs + (int64_t)bhk * D + 4 * cg);
   float2 e[ATT_MAX_CHUNKS];
   uint2 oi[ATT_MAX_CHUNKS];
 #pragma unroll
@@ -895,7 +906,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
       oi[i] = *reinterpret_cast<const uint2*>(po + (int64_t)i * ATT_BM * D);
     }
   }
-  const float cl = c0 * qs[(int64_t)bh * Sq + qrow];
+  const float cl = c0 * qsr;
   float M = -INFINITY;
 #pragma unroll
   for (int i = 0; i < ATT_MAX_CHUNKS; ++i)
@@ -915,7 +926,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     }
   }
   const float inv = L > 0.0f ? (1.0f / 448.0f) / L : 0.0f;  // a row without any visible key is written as 0
-  const v4f sc4 = *reinterpret_cast<const v4f*>(vs + (int64_t)bhk * D + 4 * cg);
   const uint32_t e0 = f32_to_out_bits<OUT_DT>((acc.x * inv) * sc4[0]);
   const uint32_t e1 = f32_to_out_bits<OUT_DT>((acc.y * inv) * sc4[1]);
   const uint32_t e2 = f32_to_out_bits<OUT_DT>((acc.z * inv) * sc4[2]);
