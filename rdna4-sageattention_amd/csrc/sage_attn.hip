@@ -1074,10 +1074,10 @@ int attn_plan_impl(int B, int H, int Sq, int Skv, int D, int causal, int* n_full
   return SAGE_OK;
 }
 
-int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t, const float* vs,
-              void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D,
-              int causal, int out_dtype, float* lse, void* workspace, int64_t workspace_bytes, void* stream) {
-  const char* who = "sage_attn_fwd";
+// Every argument check of the attention step: sage_forward runs it before its first launch as well.
+int attn_args_check(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t,
+                    const float* vs, const void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv,
+                    int Sq, int Skv, int D, int causal, int out_dtype, const char* who) {
   int rc = check_attn_shape(B, H, Hkv, Sq, Skv, D, causal, who);
   if (rc) return rc;
   if (out_dtype != SAGE_DTYPE_BF16 && out_dtype != SAGE_DTYPE_F16)
@@ -1087,6 +1087,15 @@ int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* 
                "%s: q8 / k8 / v8t / vs / out must be 16-byte aligned", who);
   SAGE_REQUIRE(osb % 8 == 0 && oss % 8 == 0 && osh % 8 == 0 && osb >= 0 && oss >= 0 && osh >= 0,
                "%s: out strides must be non-negative multiples of 8 elements", who);
+  return SAGE_OK;
+}
+
+int attn_impl(const int8_t* q8, const float* qs, const int8_t* k8, const float* ks, const uint8_t* v8t, const float* vs,
+              void* out, int64_t osb, int64_t oss, int64_t osh, int B, int H, int Hkv, int Sq, int Skv, int D,
+              int causal, int out_dtype, float* lse, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = attn_args_check(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, out_dtype,
+                           "sage_attn_fwd");
+  if (rc) return rc;
   return SAGE_ATTN_DISPATCH(D, causal, out_dtype == SAGE_DTYPE_BF16, launch_attn, q8, qs, k8, ks, v8t, vs, out, osb,
                             oss, osh, lse, B, H, Hkv, Sq, Skv, D, workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -33,6 +33,8 @@ int quant_kv_impl(const void*, int64_t, int64_t, int64_t, const void*, int64_t, 
 int attn_impl(const int8_t*, const float*, const int8_t*, const float*, const uint8_t*, const float*, void*, int64_t,
               int64_t, int64_t, int, int, int, int, int, int, int, int, float*, void*, int64_t, void*);
 int attn_plan_impl(int, int, int, int, int, int, int*, int*, int64_t*);
+int attn_args_check(const int8_t*, const float*, const int8_t*, const float*, const uint8_t*, const float*, const void*,
+                    int64_t, int64_t, int64_t, int, int, int, int, int, int, int, int, const char*);
 int64_t vamax_partial_bytes(int B, int Hkv, int Skv, int D);
 int forward_inputs_check(const void*, int64_t, int64_t, int64_t, const void*, int64_t, int64_t, int64_t, const void*,
                          int64_t, int64_t, int64_t, int, int, int, int, int, int, int, const char*);
@@ -135,6 +137,10 @@ int sage_forward(const void* q, int64_t qsb, int64_t qss, int64_t qsh, const voi
                                       "sage_forward");
   if (rc) return rc;
   if ((rc = sage::check_qs_mul(qs_mul, "sage_forward"))) return rc;
+  // the attention step's checks (its size limits, the output, the intermediates) before the quantizers launch
+  if ((rc = sage::attn_args_check(q8, qs, k8, ks, v8t, vs, out, osb, oss, osh, B, H, Hkv, Sq, Skv, D, causal, dtype,
+                                  "sage_forward")))
+    return rc;
   if (workspace == nullptr) {
     // no workspace: V maxima by atomics (four quantization launches) and every attention tile whole
     if ((rc = sage::v_amax_impl(v, vsb, vss, vsh, B, Hkv, Skv, D, dtype, vs, stream))) return rc;

@@ -129,6 +129,29 @@ def test_forward_without_workspace_checks_q_k_v_first(bad, what):
     assert what in _err()
 
 
+@pytest.mark.parametrize("bad, what", [("out", "pointer argument is NULL"), ("out_align", "16-byte aligned"),
+                                       ("oss", "out strides"), ("q8", "pointer argument is NULL"),
+                                       ("v8t", "16-byte aligned"), ("skv", "too long")])
+@pytest.mark.parametrize("with_ws", [False, True])
+def test_forward_checks_the_attention_arguments_before_launching(bad, what, with_ws):
+    # the output, the intermediates and the attention's size limits are checked before the quantizers launch (with no
+    # GPU here, a launch would fail with a HIP error instead of the argument error)
+    lib = _capi.lib()
+    skv = 2**24 if bad == "skv" else 64  # 128 channels x 2^24 keys: past the 2^31-byte V8T head the kernels index
+    inputs = (P, 0, 128, 0, P, 0, 128, 0, P, 0, 128, 0)
+    out = None if bad == "out" else P + 8 if bad == "out_align" else P
+    osb, oss, osh = 0, (100 if bad == "oss" else 128), 128
+    inter = [P] * 6
+    if bad == "q8":
+        inter[0] = None
+    if bad == "v8t":
+        inter[4] = P + 4
+    ws, ws_bytes = (P, 1 << 40) if with_ws else (None, 0)
+    rc = lib.sage_forward(*inputs, out, osb, oss, osh, 1, 4, 2, 64, skv, 128, 0, 0, 1.0, *inter, ws, ws_bytes, None)
+    assert rc == _capi.SAGE_ERR_INVALID, _err()
+    assert what in _err(), _err()
+
+
 def test_varlen_layout_bounds():
     """Padded key rows: sum of the sequences' lengths rounded up to 128 is at most total + 127 * batch; query tiles:
     sum of ceil(len / 128) is at most (total + 127 * batch) / 128.  Tables are 256-byte aligned regions."""
