@@ -107,3 +107,37 @@ def make_inputs(cfg: Config, heads: slice | None = None):
         k, v = k[:, heads], v[:, heads]
         q = q[:, heads.start * grp: heads.stop * grp]
     return q, k, v
+
+
+# The model shapes of the reference's benchmark (tests/bench_models.py:15-42): name, B, Sq, Skv, H, D, layout,
+# dtype name, causal.  bench.py --models times them with the reference's method (3 warm-ups, median of 10 calls each
+# followed by a synchronisation, tests/bench_models.py:45-53) on random N(0, 1) inputs; tests/test_gpu_models.py
+# checks the kernel on each of them against the oracle.
+MODEL_SHAPES = [
+    ("SD1.5 512 (d40->sdpa)", 2, 4096, 4096, 8, 40, "NHD", "f16", False),
+    ("SDXL 1024 lvl1 self", 2, 4096, 4096, 10, 64, "NHD", "f16", False),
+    ("SDXL 1024 lvl2 self", 2, 1024, 1024, 20, 64, "NHD", "f16", False),
+    ("SDXL 1024 lvl1 cross77", 2, 4096, 77, 10, 64, "NHD", "f16", False),
+    ("SD3.5L joint", 2, 4250, 4250, 38, 64, "NHD", "f16", False),
+    ("Flux 1024 joint", 1, 4352, 4352, 24, 128, "HND", "bf16", False),
+    ("Flux 768 joint", 1, 2560, 2560, 24, 128, "HND", "bf16", False),
+    ("Flux 512 joint", 1, 1280, 1280, 24, 128, "HND", "bf16", False),
+    ("Flux.2 1024 joint", 1, 4608, 4608, 48, 128, "HND", "bf16", False),
+    ("Qwen-Image 1328 joint", 1, 6989, 6989, 24, 128, "HND", "bf16", False),
+    ("HiDream 1024 joint", 1, 4480, 4480, 20, 128, "NHD", "bf16", False),
+    ("Neta Lumina 1024", 1, 4352, 4352, 24, 96, "HND", "bf16", False),
+    ("Anima 1024 self", 2, 4096, 4096, 16, 128, "HND", "bf16", False),
+    ("Anima 1024 cross512", 2, 4096, 512, 16, 128, "HND", "bf16", False),
+    ("Wan1.3B 480p self", 1, 32760, 32760, 12, 128, "NHD", "f16", False),
+    ("Wan1.3B 480p cross512", 1, 32760, 512, 12, 128, "NHD", "f16", False),
+    ("Wan14B 480p self", 1, 32760, 32760, 40, 128, "NHD", "f16", False),
+    ("Wan2.2-5B 704p self", 1, 27280, 27280, 24, 128, "NHD", "f16", False),
+    ("HunyuanVideo 544p", 1, 67320, 67320, 24, 128, "HND", "bf16", False),
+    ("LTXV-2B 768x512x97", 1, 4992, 4992, 32, 64, "NHD", "bf16", False),
+    ("LTXV-2B cross128", 1, 4992, 128, 32, 64, "NHD", "bf16", False),
+    ("CogVideoX-5B joint", 1, 17776, 17776, 48, 64, "NHD", "bf16", False),
+    ("AuraFlow 1024 joint d256", 2, 4360, 4360, 12, 256, "HND", "f16", False),
+    ("causal d128 4k", 1, 4096, 4096, 32, 128, "HND", "bf16", True),
+    ("causal d128 16k", 1, 16384, 16384, 32, 128, "HND", "bf16", True),
+    ("causal d64 8k", 1, 8192, 8192, 32, 64, "HND", "bf16", True),
+]

@@ -69,6 +69,26 @@ def cosine(a, b) -> float:
     return float((a * b).sum() / np.sqrt((a * a).sum() * (b * b).sum()))
 
 
+def fp32_cos_head(q, k, v, out, causal, chunk=4096):
+    """Cosine between one head's output and float32 attention computed on the GPU in row chunks (q [Sq, D], k / v
+    [Skv, D] float32 device tensors, out [Sq, D])."""
+    sq, skv, d = q.shape[0], k.shape[0], q.shape[1]
+    kt = k.t().contiguous()
+    num = den_a = den_b = 0.0
+    for r0 in range(0, sq, chunk):
+        r1 = min(sq, r0 + chunk)
+        s = torch.matmul(q[r0:r1], kt) * (d ** -0.5)
+        if causal:
+            last = torch.arange(r0, r1, device=q.device)[:, None] + (skv - sq)
+            s = s.masked_fill(torch.arange(skv, device=q.device)[None, :] > last, float("-inf"))
+        ref = torch.matmul(torch.softmax(s, dim=-1), v)
+        o = out[r0:r1].float()
+        num += float((o * ref).sum())
+        den_a += float((o * o).sum())
+        den_b += float((ref * ref).sum())
+    return num / (den_a * den_b) ** 0.5
+
+
 def kv_split(dev, B, H, Sq, Skv, D, causal, heads=None):
     """The emulation's ``kv_split`` argument that follows the attention kernel's plan on `dev` (None when the plan
     splits nothing).  ``heads``: indices, in the full problem of H heads, of the heads an emulated sample holds."""

@@ -17,7 +17,7 @@ import torch
 import sageattention
 from cdna4_sage import _capi
 from cdna4_sage.configs import CONFIGS, make_inputs
-from gpu_util import assert_near_walk, kv_split, run_quant_kv, run_quant_q
+from gpu_util import assert_near_walk, fp32_cos_head, kv_split, run_quant_kv, run_quant_q
 from oracle import sage_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -25,26 +25,6 @@ pytestmark = pytest.mark.gpu
 MAX_ABS = 2e-2
 COS = 0.999
 BM = 128  # query rows per attention workgroup
-
-
-def _fp32_cos_head(q, k, v, out, causal, chunk=4096):
-    """Cosine between one head's output and float32 attention computed on the GPU in row chunks (q [Sq, D], k / v
-    [Skv, D] float32 device tensors, out [Sq, D])."""
-    sq, skv, d = q.shape[0], k.shape[0], q.shape[1]
-    kt = k.t().contiguous()
-    num = den_a = den_b = 0.0
-    for r0 in range(0, sq, chunk):
-        r1 = min(sq, r0 + chunk)
-        s = torch.matmul(q[r0:r1], kt) * (d ** -0.5)
-        if causal:
-            last = torch.arange(r0, r1, device=q.device)[:, None] + (skv - sq)
-            s = s.masked_fill(torch.arange(skv, device=q.device)[None, :] > last, float("-inf"))
-        ref = torch.matmul(torch.softmax(s, dim=-1), v)
-        o = out[r0:r1].float()
-        num += float((o * ref).sum())
-        den_a += float((o * o).sum())
-        den_b += float((ref * ref).sum())
-    return num / (den_a * den_b) ** 0.5
 
 
 def _tiles(cfg, n_full, head_flat):
@@ -119,7 +99,7 @@ def test_config_full_workload(dev, name):
             print(f"config {name} b={b} head {hq}: {int(sel.sum())} split rows, max |out - walk| = {gap:.3g}",
                   flush=True)
         # cosine against float32 attention over the whole head
-        cos = _fp32_cos_head(qd[b, hq].float(), kd[b, hk].float(), vd[b, hk].float(), out[b, hq], cfg.causal)
+        cos = fp32_cos_head(qd[b, hq].float(), kd[b, hk].float(), vd[b, hk].float(), out[b, hq], cfg.causal)
         assert cos >= COS, (name, b, hq, cos)
         if lse is not None:
             qr = q1[0, 0, rows].double().numpy()
