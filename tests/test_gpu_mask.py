@@ -150,6 +150,61 @@ def test_flux_size_identities(dev):
     assert (none == 0).all()
 
 
+@pytest.mark.parametrize("kind", ["bool", "float"])
+def test_flux_size_key_masks_vs_emulation(dev, kind):
+    """Config 2 (Flux 1x24x4608x128) at full size with bench.py's key-padding mask (the first 4032 of 4608 keys
+    visible) or an additive per-key bias of the inputs' dtype (+-2 on those keys, -inf on the rest), against the
+    emulation with the same mask on sampled query tiles of two heads: the first, middle and last tile and the split
+    tiles of the plan; split rows also against the one walk, and float32 masked attention over the whole head."""
+    from cdna4_sage.configs import CONFIGS, make_inputs
+    cfg = CONFIGS["2"]
+    S, D = cfg.S, cfg.D
+    q, k, v = make_inputs(cfg)
+    vis = torch.arange(S) < S - S // 8
+    if kind == "bool":
+        mask = vis
+    else:
+        g = torch.Generator().manual_seed(12)
+        mask = torch.where(vis, torch.rand(S, generator=g) * 4 - 2, torch.tensor(float("-inf"))).to(cfg.dtype)
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), mask.to(dev)
+    out = cdna4_sage.attention(qd, kd, vd, attn_mask=md)
+    assert torch.isfinite(out).all()
+    n_full, _, _ = _capi.attn_plan(dev.index or 0, cfg.B, cfg.H, S, S, D, False)
+    m = mask.numpy() if kind == "bool" else mask.float().numpy()
+    q_tiles = S // 128
+    for h in (0, cfg.H - 1):
+        pick = {0, q_tiles // 2, q_tiles - 1}
+        first_split = n_full - h * q_tiles
+        if 0 < first_split < q_tiles:
+            pick |= {first_split - 1, first_split}
+        rows = np.concatenate([np.arange(t * 128, (t + 1) * 128) for t in sorted(pick)])
+        qn, kn, vn = (t[:, h:h + 1].float().numpy() for t in (q, k, v))
+        q8, qs = orc.quant_q(qn)
+        k8, ks, v8, vs = orc.quant_kv(kn, vn, seq_pad=_capi.kv_pad(S))
+        split = kv_split(dev, cfg.B, cfg.H, S, S, D, False, heads=[h])
+        if split is not None:
+            split = (split[0], split[1][:, :, rows])
+        # the mask does not depend on the query row, so whole sampled tiles stand for a query sequence of their own
+        emu = orc.attention(np.ascontiguousarray(q8[:, :, rows]), np.ascontiguousarray(qs[:, :, rows]), k8, ks, v8, vs,
+                            S, block_n=32, kv_split=split, attn_mask=m[None, None, None, :],
+                            also_unsplit=split is not None)
+        emu, walk = emu if split is not None else (emu, None)
+        got = out[0, h][torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+        err = float(np.abs(got - emu[0, 0]).max())
+        same = float((got == emu[0, 0]).mean())
+        print(f"flux {kind} mask head {h}: {len(rows)} rows, max |out - emu| = {err:.3g}, bit-equal {same:.4f}",
+              flush=True)
+        assert err <= MAX_ABS and same >= SAME_BITS[cfg.dtype], (h, err, same)
+        if walk is not None and split[1].any():
+            sel = split[1][0, 0]
+            ref = orc.sdpa_reference(qn[:, :, rows[sel]], kn, vn, attn_mask=m[None, None, None, :])[0, 0]
+            assert_near_walk(got[sel], walk[0, 0][sel], ref)
+        fm = md if kind == "bool" else md.float()
+        ref32 = F.scaled_dot_product_attention(qd[:, h:h + 1].float(), kd[:, h:h + 1].float(), vd[:, h:h + 1].float(),
+                                               attn_mask=fm)
+        assert cosine(out[:, h:h + 1].float().cpu().numpy(), ref32.cpu().numpy()) >= COS
+
+
 def test_fully_masked_rows_and_tiles_give_zero(dev):
     q, k, v = (t.to(dev) for t in _inputs(2, 2, 2, 300, 600, 64, torch.float16, "HND", seed=6))
     none = torch.zeros(2, 1, 1, 600, dtype=torch.bool, device=dev)
