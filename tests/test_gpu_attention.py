@@ -95,6 +95,41 @@ def test_attention_vs_emulation(dev, B, H, Hkv, Sq, Skv, D, dt, layout, causal):
         assert_near_walk(got, walk, ref)
 
 
+@pytest.mark.parametrize("D,dt,causal", [(128, torch.bfloat16, False), (64, torch.float16, True),
+                                         (96, torch.bfloat16, False), (256, torch.float16, False)])
+def test_degenerate_inputs_vs_emulation(dev, D, dt, causal):
+    """Inputs that reach the quantizers' clamps, through the whole forward: zero query rows (scale 1e-12 / 127, every
+    score of the row 0, so uniform weights over the visible keys), a zero 32-key K block (scale 1e-12 / 127, those
+    scores 0), a head whose keys are all equal (uniform weights on every row), a zero V channel (VS = 0: that output
+    channel is exactly 0) and a constant V channel (every E4M3 code 448).  Against the emulation and float64
+    attention with the gates above."""
+    B, H, Hkv, Sq, Skv = 1, 2, 2, 300, 333
+    g = torch.Generator().manual_seed(31 + D)
+    q = torch.randn(B, H, Sq, D, generator=g)
+    k = torch.randn(B, Hkv, Skv, D, generator=g)
+    v = torch.randn(B, Hkv, Skv, D, generator=g)
+    q[:, :, 10] = 0.0
+    q[:, 1, 200:260] = 0.0
+    k[:, 0, 64:96] = 0.0
+    k[:, 1] = k[:, 1, :1].clone()
+    v[..., 9] = 0.0
+    v[..., 17] = 0.75
+    q, k, v = (t.to(dt) for t in (q, k, v))
+    out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), is_causal=causal)
+    got = hnd_np(out)
+    assert np.isfinite(got).all()
+    assert (got[..., 9] == 0).all()
+    split = kv_split(dev, B, H, Sq, Skv, D, causal)
+    emu, ref, walk = _emulate(q, k, v, "HND", causal, out_dtype="bf16" if dt == torch.bfloat16 else "f16",
+                              split=split, walk=True)
+    err = float(np.abs(got - emu).max())
+    assert err <= MAX_ABS, err
+    assert cosine(got, ref) >= COS
+    assert float((got == emu).mean()) >= SAME_BITS[dt]
+    if walk is not None:
+        assert_near_walk(got, walk, ref)
+
+
 def test_sm_scale(dev):
     q, k, v = _inputs(1, 2, 2, 600, 600, 128, torch.bfloat16, "HND", seed=7)
     out = cdna4_sage.attention(q.to(dev), k.to(dev), v.to(dev), "HND", sm_scale=0.05)
