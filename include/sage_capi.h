@@ -9,7 +9,9 @@
  * entry points are reentrant; nothing synchronises.
  *
  * Conventions
- *  - Return value: SAGE_OK (0) or a SAGE_ERR_* code; sage_last_error() gives the message (thread-local).
+ *  - Return value: SAGE_OK (0) or a SAGE_ERR_* code; sage_last_error() gives the message (thread-local).  Every
+ *    entry point checks all of its arguments before its first launch: a call rejected with SAGE_ERR_INVALID or
+ *    SAGE_ERR_UNSUPPORTED has launched nothing and written no memory.
  *  - Memory: the caller owns every buffer (inputs, outputs, intermediates) and the library allocates nothing at run
  *    time; its only device memory is the static scratch array of sage_forward_noalloc (one per GPU it runs on).
  *  - Streams: `stream` is a hipStream_t (NULL = the default stream).
