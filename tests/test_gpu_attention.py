@@ -46,6 +46,10 @@ CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 2, 2, 200, 100, 64, torch.float16, "HND", False),      # a whole tile and a partial one
     (1, 2, 2, 128, 128, 128, torch.bfloat16, "NHD", True),     # two whole tiles, causal
     (2, 2, 1, 70, 190, 128, torch.bfloat16, "HND", True),      # three tiles, causal with q_len < kv_len
+    # wider GQA groups and a larger batch: 8 query heads per kv head (causal), multi-query (16 per kv head), batch 4
+    (2, 32, 4, 700, 700, 128, torch.bfloat16, "HND", True),
+    (1, 16, 1, 300, 900, 64, torch.float16, "NHD", False),
+    (4, 8, 2, 257, 513, 128, torch.bfloat16, "NHD", True),
 ]
 
 
