@@ -23,6 +23,9 @@ CASES = [  # B, H, Hkv, Sq, Skv, D, dtype, layout, causal
     (1, 2, 2, 96, 33, 128, torch.bfloat16, "HND", False),
     (1, 2, 2, 128, 128, 64, torch.float16, "NHD", True),
     (2, 2, 1, 70, 190, 128, torch.bfloat16, "HND", True),
+    # 8 query heads per kv head (causal, batch 2) and multi-query
+    (2, 16, 2, 600, 600, 128, torch.bfloat16, "HND", True),
+    (1, 16, 1, 300, 900, 64, torch.float16, "NHD", False),
 ]
 
 
